@@ -1,0 +1,282 @@
+#!/usr/bin/env python3
+"""Benchmark of the W4A16 linear-layer hot path on one MI355X.
+
+Headline (value): BASELINE config 2 -- the Qwen2.5-7B-shaped decode linear set at M=1 (fused
+QKV 4608x3584, O 3584x3584, fused gate+up 37888x3584, down 3584x18944; int4 group 128). One
+"step" is one pass of the four ns_w4_linear launches over one batch. value = algorithmic bytes
+of the step / step time, in GB/s. Inputs are resident in HBM; weight copies rotate over
+>= 1.1 GiB so each step reads HBM, not the 256 MB Infinity Cache.
+
+Timing: warmup steps, then exactly --steps steps, each group captured in a HIP graph (no host
+launch gaps inside the timed region), bracketed by synchronize() and HIP events recorded on
+the stream the kernels run on. Also reported under "extra": per-layer launch durations,
+the M=8 set (config 3), the 1.5B gate (config 1), the prefill GEMMs (config 4) and the same
+M=1 step launched eagerly from Python.
+
+roofline: the dominant kernel (gate+up GEMV, M=1): algorithmic bytes per launch / its average
+launch duration (HIP events around a graph of back-to-back launches on rotating copies),
+against 8 TB/s. cpu_baseline: the PyTorch-CPU dequant+matmul restatement of the reference's
+CPU loop (oracle/w4_oracle.py), timed on this host's cores on the full M=1 set.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA (256 CU x 4096 flop/clk x 2.4 GHz)
+G = 128
+ROTATE_BYTES = int(1.1 * (1 << 30))
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-extra", action="store_true", help="headline only")
+    p.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU baseline time budget")
+    return p.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus}: this build measures one GPU only (each GPU box has "
+              "one MI355X); multi-GPU sharding is design-only.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from nanoserve_amd import Kernels, synth
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.set_device(0)
+    kern = Kernels()
+    dev = torch.device("cuda", 0)
+
+    def dev_bits(a, dtype):
+        view = {np.dtype(np.uint16): np.int16, np.dtype(np.uint32): np.int32}[a.dtype]
+        return torch.from_numpy(np.ascontiguousarray(a).view(view)).view(dtype).to(dev)
+
+    layers = synth.QWEN7B_LAYERS
+    set_bytes = sum(N * K // 2 + N * (K // G) * 2 for _, N, K in layers)
+    copies = max(2, -(-ROTATE_BYTES // set_bytes))
+
+    # Host inputs (one seeded draw per layer), device copies rotated for timing.
+    host_w = {name: synth.weights(N, K, G, seed=10 + i) for i, (name, N, K) in enumerate(layers)}
+    dev_w = {name: [] for name, _, _ in layers}
+    for name, N, K in layers:
+        Wq, S = host_w[name]
+        wq0, s0 = dev_bits(Wq, torch.int32), dev_bits(S, torch.bfloat16)
+        dev_w[name].append((wq0, s0))
+        for _ in range(copies - 1):
+            dev_w[name].append((wq0.clone(), s0.clone()))
+    x1 = {name: dev_bits(synth.activations(1, K, seed=100 + i), torch.bfloat16)
+          for i, (name, N, K) in enumerate(layers)}
+    x8 = {name: dev_bits(synth.activations(8, K, seed=200 + 8 * i, per_row_seed=True),
+                         torch.bfloat16) for i, (name, N, K) in enumerate(layers)}
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+
+    def step(xs, i, which=None):
+        for name, N, K in layers:
+            if which is not None and name != which:
+                continue
+            wq, s = dev_w[name][i % copies]
+            kern.w4_linear(xs[name], wq, s, G)
+
+    def graph_of(fn, n):
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn(0)  # allocator warm-up outside capture
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn(i)
+        torch.cuda.synchronize()
+        return g
+
+    def time_graph(g, reps=1):
+        st = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(st)
+        for _ in range(reps):
+            g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1)  # ms
+
+    # ---------------- headline: M=1 set, exactly args.steps steps
+    g_warm = graph_of(lambda i: step(x1, i), max(args.warmup, 1))
+    g_main = graph_of(lambda i: step(x1, i), args.steps)
+    if args.warmup > 0:
+        time_graph(g_warm)
+    ms_total = time_graph(g_main)
+    ms_step = ms_total / args.steps
+    bytes_m1 = sum(synth.gemv_bytes(1, N, K, G) for _, N, K in layers)
+    value = bytes_m1 / (ms_step * 1e-3) / 1e9
+
+    # ---------------- dominant kernel: gate+up GEMV, M=1, back-to-back launches
+    n_launch = 4 * copies
+    g_gu = graph_of(lambda i: step(x1, i, which="gate_up"), n_launch)
+    time_graph(g_gu)
+    ms_gu = statistics.median(time_graph(g_gu) for _ in range(5)) / n_launch
+    N_gu, K_gu = [(N, K) for n, N, K in layers if n == "gate_up"][0]
+    bytes_gu = synth.gemv_bytes(1, N_gu, K_gu, G)
+    achieved = bytes_gu / (ms_gu * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "w4_gemv_mfma_kernel (gate_up 37888x3584, M=1)",
+                "bytes_per_launch": bytes_gu, "avg_launch_us": round(ms_gu * 1e3, 3)}
+
+    extra = {}
+    if not args.no_extra:
+        per_layer = {}
+        for name, N, K in layers:
+            for M, xs in ((1, x1), (8, x8)):
+                g = graph_of(lambda i, name=name, xs=xs: step(xs, i, which=name), n_launch)
+                time_graph(g)
+                ms = statistics.median(time_graph(g) for _ in range(3)) / n_launch
+                b = synth.gemv_bytes(M, N, K, G)
+                per_layer[f"{name}_m{M}"] = {"us": round(ms * 1e3, 3),
+                                             "gbs": round(b / (ms * 1e-3) / 1e9, 1),
+                                             "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        extra["per_layer"] = per_layer
+
+        g8 = graph_of(lambda i: step(x8, i), 4 * copies)
+        time_graph(g8)
+        ms8 = statistics.median(time_graph(g8) for _ in range(3)) / (4 * copies)
+        bytes_m8 = sum(synth.gemv_bytes(8, N, K, G) for _, N, K in layers)
+        extra["config3_m8_set"] = {"gbs": round(bytes_m8 / (ms8 * 1e-3) / 1e9, 1),
+                                   "us_per_step": round(ms8 * 1e3, 3),
+                                   "frac_hbm": round(bytes_m8 / (ms8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+        # eager launches (Python + ctypes per call), for reference only
+        for i in range(10):
+            step(x1, i)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(x1, i)
+        torch.cuda.synchronize()
+        ms_eager = (time.perf_counter() - t0) * 1e3 / args.steps
+        extra["config2_m1_eager_gbs"] = round(bytes_m1 / (ms_eager * 1e-3) / 1e9, 1)
+
+        # config 1: Qwen2.5-1.5B gate, M=1
+        name, N, K = synth.QWEN15B_GATE
+        Wq, S = synth.weights(N, K, G, seed=1)
+        c1b = N * K // 2 + N * (K // G) * 2
+        c1n = max(2, -(-ROTATE_BYTES // c1b))
+        wq0, s0 = dev_bits(Wq, torch.int32), dev_bits(S, torch.bfloat16)
+        c1w = [(wq0, s0)] + [(wq0.clone(), s0.clone()) for _ in range(c1n - 1)]
+        xc1 = dev_bits(synth.activations(1, K, seed=3), torch.bfloat16)
+        g1 = graph_of(lambda i: kern.w4_linear(xc1, *c1w[i % c1n], G), 2 * c1n)
+        time_graph(g1)
+        ms1 = statistics.median(time_graph(g1) for _ in range(3)) / (2 * c1n)
+        b1 = synth.gemv_bytes(1, N, K, G)
+        extra["config1_gate_m1"] = {"us": round(ms1 * 1e3, 3), "gbs": round(b1 / (ms1 * 1e-3) / 1e9, 1)}
+        del c1w, wq0, s0
+
+        # config 4: prefill GEMMs
+        gemm = {}
+        for name, N, K in layers:
+            if name not in ("gate_up", "down"):
+                continue
+            for M in (512, 2048):
+                xa = dev_bits(synth.activations(M, K, seed=M), torch.bfloat16)
+                ws = dev_w[name]
+                reps = 6
+                g = graph_of(lambda i: kern.w4_linear(xa, *ws[i % copies], G), reps)
+                time_graph(g)
+                ms = statistics.median(time_graph(g) for _ in range(3)) / reps
+                tf = synth.gemm_flops(M, N, K) / (ms * 1e-3) / 1e12
+                gemm[f"{name}_m{M}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
+                                        "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+                del xa
+        extra["config4_gemm"] = gemm
+
+    # ---------------- CPU baseline (PyTorch CPU dequant + fp32 matmul), full M=1 set
+    cpu = None
+    if not args.no_cpu:
+        from oracle.w4_oracle import torch_cpu_linear
+
+        cpu_in = []
+        for name, N, K in layers:
+            Wq, S = host_w[name]
+            cpu_in.append((torch.from_numpy(synth.activations(1, K, seed=100).view(np.int16).copy()).view(torch.bfloat16),
+                           torch.from_numpy(Wq.view(np.int32).copy()),
+                           torch.from_numpy(S.view(np.int16).copy()).view(torch.bfloat16)))
+
+        def cpu_step():
+            for x, wq, s in cpu_in:
+                torch_cpu_linear(x, wq, s, G)
+
+        cpu_step()  # warmup
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 5 or (time.perf_counter() - t_start < args.cpu_seconds and len(times) < 50):
+            t0 = time.perf_counter()
+            cpu_step()
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - t_start > 3 * args.cpu_seconds:
+                break
+        med = statistics.median(times)
+        model = platform.processor() or ""
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        model = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+        cpu = {"value": round(bytes_m1 / med / 1e9, 2), "unit": "GB/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": f"full config-2 M=1 set (4 layers), median of {len(times)} runs, "
+                         f"{med * 1e3:.1f} ms/step; PyTorch CPU unpack + (q-8)*s fp32 + fp32 matmul",
+               "os_cpu_count": os.cpu_count(), "cpu_model": model}
+
+    line = {
+        "metric": "W4A16 GEMV HBM GB/s (% of peak) at M=1/8; prefill GEMM TFLOP/s (% MFMA)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded int4 nibbles, |N(0,1)|*0.02 bf16 scales, N(0,1) bf16 activations)",
+        "config": {"workload": "config2: Qwen2.5-7B-shaped decode linear set, M=1, W4 group 128 "
+                               "(qkv 4608x3584, o 3584x3584, gate_up 37888x3584, down 3584x18944)",
+                   "frac_hbm": round(value / HBM_PEAK_GBS, 4), "bytes_per_step": bytes_m1,
+                   "weight_copies": copies, "timing": "hip graph replay, hip events"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

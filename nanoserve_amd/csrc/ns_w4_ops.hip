@@ -1,0 +1,59 @@
+// C ABI of the W4A16 engine: the drop-in boundary for csrc/nanoserve_ops.cu:65-90 of the
+// reference. Declarations and the full contract are in include/nanoserve_w4.h.
+//
+// Every argument check happens before the first HIP call, so the error paths run (and are
+// tested) on a machine without a GPU; HIP itself initialises lazily on the first launch.
+#include <stdint.h>
+
+#include "../../include/nanoserve_w4.h"
+#include "w4_kernels.h"
+
+namespace {
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int last_status() { return static_cast<int>(hipGetLastError()); }
+
+}  // namespace
+
+extern "C" {
+
+int ns_w4_quantize(const void* W, void* Wq, void* S, int N, int K, int G, void* stream) {
+  if (G <= 0 || N < 0 || K < 0) return -1;
+  if (K % G || G % 32) return -1;  // the reference's own rejection (nanoserve_ops.cu:67)
+  if (N == 0 || K == 0) return 0;
+  if (!W || !Wq || !S || !aligned(W, 16) || !aligned(Wq, 4) || !aligned(S, 2)) return -1;
+  const hipError_t e =
+      ns::launch_quantize(static_cast<const uint16_t*>(W), static_cast<uint32_t*>(Wq),
+                          static_cast<uint16_t*>(S), N, K, G, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return static_cast<int>(e);
+  return last_status();
+}
+
+int ns_w4_linear(const void* X, const void* Wq, const void* S, void* Y, int M, int N, int K,
+                 int G, void* stream) {
+  if (M <= 0 || N <= 0 || K <= 0 || G <= 0) return -2;
+  if (!X || !Wq || !S || !Y) return -2;
+  if (!aligned(X, 16) || !aligned(Wq, 16) || !aligned(S, 2) || !aligned(Y, 2)) return -2;
+  const bool fmt_ok = K % 32 == 0 && G % 32 == 0 && K % G == 0;
+  const auto st = static_cast<hipStream_t>(stream);
+  const auto x = static_cast<const uint16_t*>(X);
+  const auto wq = static_cast<const uint32_t*>(Wq);
+  const auto s = static_cast<const uint16_t*>(S);
+  const auto y = static_cast<uint16_t*>(Y);
+  hipError_t e;
+  if (M <= 8) {
+    if (!fmt_ok) return -2;
+    const ns::GemvArgs a{x, wq, s, y, M, N, K, G};
+    e = ns::launch_gemv(a, ns::gemv_plan(M, N, K, G), st);
+  } else if (M % 128 == 0 && N % 128 == 0 && fmt_ok) {
+    const ns::GemmArgs a{x, wq, s, y, M, N, K, G};
+    e = ns::launch_gemm(a, ns::gemm_plan(M, N, K, G), st);
+  } else {
+    return -2;
+  }
+  if (e != hipSuccess) return static_cast<int>(e);
+  return last_status();
+}
+
+}  // extern "C"

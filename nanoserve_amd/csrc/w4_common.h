@@ -1,0 +1,59 @@
+// Shared device helpers for the W4A16 kernels (gfx950 / CDNA4, wave64).
+//
+// Weight format (kernels/quant/w4a16.cuh:5-9 in the reference):
+//   Wq [N][K/8] uint32: word j of row n holds k = 8j..8j+7, k = 8j+i in bits 4i..4i+3
+//   S  [N][K/G] bf16:   one scale per G consecutive k
+//   w[n][k] = (q - 8) * S[n][k / G],  q in [0, 15]
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ns {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h16) {
+  return __uint_as_float(h16 << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet (the reference's
+// __float2bfloat16 / __floats2bfloat162_rn semantics, kernels/fused/vec.cuh:14-19).
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// Two fp32 -> packed bf16x2 (lo in bits 0..15), RNE. An fp32 -> bf16 vector truncation, which
+// gfx950 lowers to its single v_cvt_pk_bf16_f32 (round to nearest even).
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const f32x2_t f = {lo, hi};
+  const bf16x2_t v = __builtin_convertvector(f, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// One packed word (8 nibbles, k ascending) -> four bf16x2 dwords holding (128 + q) exactly:
+// dword j = bf16(128 + q[2j]) | bf16(128 + q[2j+1]) << 16. bf16(128 + q) is 0x4300 | q for
+// q in [0, 15] (exponent 2^7, q in the low mantissa bits), so no arithmetic is needed:
+// one byte permute places nibble 2j (byte j of w) and nibble 2j+1 (byte j of w >> 4) in the
+// low nibbles of the two halves, one AND-OR masks them and sets the exponent.
+__device__ __forceinline__ void unpack_word_128q(uint32_t w, uint32_t (&d)[4]) {
+  const uint32_t w4 = w >> 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    // selector bytes: out0 <- w.byte j, out1 <- 0, out2 <- w4.byte j, out3 <- 0
+    const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + j) << 16) | (uint32_t)j;
+    const uint32_t t = __builtin_amdgcn_perm(w4, w, sel);
+    d[j] = (t & 0x000F000Fu) | 0x43004300u;
+  }
+}
+
+}  // namespace ns

@@ -1,0 +1,45 @@
+// Host-side interface between the C ABI (ns_w4_ops.hip) and the kernel files.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ns {
+
+struct GemvArgs {
+  const uint16_t* X;
+  const uint32_t* Wq;
+  const uint16_t* S;
+  uint16_t* Y;
+  int M, N, K, G;
+};
+
+struct GemvPlan {
+  bool fast;  // MFMA kernel (K % 128 == 0, G % 128 == 0); otherwise the generic kernel
+  int rt;     // 16-row tiles per wavefront
+  int nw;     // wavefronts per workgroup splitting K
+};
+
+bool gemv_fast_path_ok(int M, int N, int K, int G);
+GemvPlan gemv_plan(int M, int N, int K, int G);
+hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st);
+
+struct GemmArgs {
+  const uint16_t* A;   // X [M][K] bf16
+  const uint32_t* Wq;  // [N][K/8]
+  const uint16_t* S;   // [N][K/G] bf16
+  uint16_t* C;         // Y [M][N] bf16
+  int M, N, K, G;
+};
+
+struct GemmPlan {
+  int cfg;  // index into the tile-configuration table of w4_gemm.hip
+  int bm, bn;
+};
+
+GemmPlan gemm_plan(int M, int N, int K, int G);
+hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st);
+
+hipError_t launch_quantize(const uint16_t* W, uint32_t* Wq, uint16_t* S, int N, int K, int G,
+                           hipStream_t st);
+
+}  // namespace ns
