@@ -60,12 +60,15 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm_kernel(
   static_assert(A_CHUNKS % THREADS == 0, "even activation-tile split");
   __shared__ __align__(16) uint16_t As[2][BM * LDA];
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int KW = K >> 3, KG = K / G;
   const int KB = (K + BK - 1) / BK;
 
-  // ---- activation tile loader (global -> registers -> LDS)
+  // ---- activation tile loader (global -> registers -> LDS). Every load is issued for every
+  // lane (addresses clamped into the tensor), so the number of loads in flight never depends
+  // on the path; columns past K (only when K % 64 == 32) are zeroed when stored to LDS.
   const uint16_t* a_src[A_PER_THREAD];
   int a_dst[A_PER_THREAD], a_col[A_PER_THREAD];
 #pragma unroll
@@ -81,18 +84,24 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm_kernel(
   auto load_a = [&](int kb) {
 #pragma unroll
     for (int p = 0; p < A_PER_THREAD; ++p) {
-      const int k = kb * BK + a_col[p];
-      a_reg[p] = k < K ? *reinterpret_cast<const u32x4_t*>(a_src[p] + kb * BK)
-                       : u32x4_t{0u, 0u, 0u, 0u};
+      const int k0 = kb * BK + a_col[p] < K ? kb * BK : 0;
+      a_reg[p] = *reinterpret_cast<const u32x4_t*>(a_src[p] + k0);
     }
   };
-  auto store_a = [&](int stage) {
+  auto store_a = [&](int stage, int kb) {
+    if ((kb + 1) * BK > K) {  // tail block: zero the columns past K
+#pragma unroll
+      for (int p = 0; p < A_PER_THREAD; ++p)
+        if (kb * BK + a_col[p] >= K) a_reg[p] = u32x4_t{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
     for (int p = 0; p < A_PER_THREAD; ++p)
       *reinterpret_cast<u32x4_t*>(&As[stage][a_dst[p]]) = a_reg[p];
   };
 
-  // ---- weight loader: lane (n = lane % 32, kh = lane / 32), one 16-byte load per n-frag
+  // ---- weight loader: lane (n = lane % 32, kh = lane / 32), one 16-byte load per n-frag.
+  // Words past the row end (K % 64 == 32 tail) are read from the row start instead; they meet
+  // zero activations.
   const int ln = lane & 31, kh = lane >> 5;
   const u32x4_t* w_src[NJ];
   const uint16_t* s_src[NJ];
@@ -102,15 +111,17 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm_kernel(
     w_src[j] = reinterpret_cast<const u32x4_t*>(Wq + (size_t)n * KW);
     s_src[j] = S + (size_t)n * KG;
   }
-  u32x4_t w_reg[NJ];
-  float s_reg[NJ];
-  auto load_w = [&](int kb) {
-    const int word = kb * (BK / 8) + 4 * kh;  // first of this lane's 4 words
-    const bool in = word < KW;                // K % 32 == 0: a 4-word run is all in or all out
+  struct WRegs {
+    u32x4_t w[NJ];
+    uint32_t s[NJ];  // bf16 bits of the group scale
+  };
+  auto load_w = [&](WRegs& r, int kb) {
+    int word = kb * (BK / 8) + 4 * kh;  // first of this lane's 4 words
+    word = word < KW ? word : 0;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      w_reg[j] = w_src[j][in ? (word >> 2) : 0];
-      s_reg[j] = bf16_bits_to_f32(s_src[j][in ? (word * 8) / G : 0]);
+      r.w[j] = w_src[j][word >> 2];
+      r.s[j] = s_src[j][(word * 8) / G];
     }
   };
 
@@ -122,30 +133,16 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  load_a(0);
-  load_w(0);
-  store_a(0);
-  __syncthreads();
-
-  for (int kb = 0; kb < KB; ++kb) {
-    const int st = kb & 1;
-    u32x4_t w_cur[NJ];
-    float s_cur[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      w_cur[j] = w_reg[j];
-      s_cur[j] = s_reg[j];
-    }
-    if (kb + 1 < KB) {
-      load_a(kb + 1);
-      load_w(kb + 1);
-    }
-    const uint16_t* as = As[st];
+  auto compute = [&](int stage, const WRegs& r) {
+    const uint16_t* as = As[stage];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       u32x4_t bfrag[NJ];
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) bfrag[j] = dequant_word_bf16(w_cur[j][s], s_cur[j], -8.f * s_cur[j]);
+      for (int j = 0; j < NJ; ++j) {
+        const float sc = bf16_bits_to_f32(r.s[j]);
+        bfrag[j] = dequant_word_bf16(r.w[j][s], sc, -8.f * sc);
+      }
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const u32x4_t afrag =
@@ -156,9 +153,36 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm_kernel(
                                                               acc[i][j], 0, 0, 0);
       }
     }
-    if (kb + 1 < KB) store_a(st ^ 1);
+  };
+
+  // ---- main loop, unrolled by two K blocks: LDS stage and weight registers alternate, so no
+  // in-flight register is ever copied. Weights are loaded two blocks ahead, activations one.
+  const int klast = KB - 1;
+  WRegs wb0, wb1;
+  load_w(wb0, 0);
+  load_w(wb1, min(1, klast));
+  load_a(0);
+  store_a(0, 0);
+  __syncthreads();
+  int kb = 0;
+  for (; kb + 1 < KB; kb += 2) {
+    load_a(kb + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(0, wb0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(wb0, min(kb + 2, klast));
+    store_a(1, kb + 1);
+    __syncthreads();
+
+    load_a(min(kb + 2, klast));
+    __builtin_amdgcn_sched_barrier(0);
+    compute(1, wb1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(wb1, min(kb + 3, klast));
+    store_a(0, min(kb + 2, klast));
     __syncthreads();
   }
+  if (kb < KB) compute(0, wb0);  // odd KB: the last block is in stage 0 / wb0
 
   // ---- epilogue: D[i][j] of lane l, register r: j = l % 32, i = 8 (r / 4) + 4 (l / 32) + r % 4
 #pragma unroll

@@ -16,8 +16,8 @@
 //    offset, so the chunk partial is sum_k x * (q - 8) exactly as the reference's integer
 //    dequant, and the bf16 group scale is applied in fp32 after the chunk. No weight is ever
 //    rounded: the dequant is exact, as in the reference GEMV (w4a16.cuh:28-32).
-//  * Loads of W and X are issued UB chunks ahead of use (registers), so each wave keeps
-//    UB x RT KiB of HBM reads in flight.
+//  * Loads of W and X are issued in batches of UB chunks, so each wave has up to UB x RT KiB
+//    of HBM reads in flight; several waves per SIMD overlap one another's batches.
 //  * Scales for the workgroup's rows are staged once in LDS, transposed to [group][row] so a
 //    lane reads its four rows' scales with one 8-byte LDS read.
 //
@@ -41,10 +41,11 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_mfma_kernel(
   constexpr int ROWS = 16 * RT;
   extern __shared__ __align__(16) unsigned char smem[];
   const int KG = K / G;
-  uint16_t* sl = reinterpret_cast<uint16_t*>(smem);  // [KG][ROWS]
-  float* red = reinterpret_cast<float*>(smem + ((KG * ROWS * 2 + 15) & ~15));  // [NW][RT][4][64]
+  uint16_t* sl = reinterpret_cast<uint16_t*>(smem);  // [KG + 1][ROWS], group KG is all zero
+  float* red = reinterpret_cast<float*>(smem + (((KG + 1) * ROWS * 2 + 15) & ~15));  // [NW][RT][4][64]
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar chunk math
   const int n0 = blockIdx.x * ROWS;
 
   // Stage this tile's scales: rows n0..n0+ROWS-1 are one contiguous run of S.
@@ -52,6 +53,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_mfma_kernel(
     const int row = e / KG, g = e - row * KG;
     sl[g * ROWS + row] = (n0 + row < N) ? S[(size_t)n0 * KG + e] : (uint16_t)0;
   }
+  for (int e = tid; e < ROWS; e += NW * kWave) sl[KG * ROWS + e] = 0;
   __syncthreads();
 
   const int r16 = lane & 15, h = lane >> 4;
@@ -65,63 +67,58 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_mfma_kernel(
     const int row = min(n0 + 16 * rt + r16, N - 1);  // rows past N are computed and dropped
     wp[rt] = reinterpret_cast<const u32x4_t*>(Wq + (size_t)row * (K >> 3)) + h;
   }
-  const bool xok = r16 < M;
-  const u32x4_t* xp = reinterpret_cast<const u32x4_t*>(X + (size_t)(xok ? r16 : 0) * K) + 4 * h;
+  // Batch columns j >= M of the MFMA are computed on a duplicate of row M-1 and never stored:
+  // every lane loads valid memory, so no load needs a per-lane predicate.
+  const u32x4_t* xp =
+      reinterpret_cast<const u32x4_t*>(X + (size_t)min(r16, M - 1) * K) + 4 * h;
 
   f32x4_t acc[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const u32x4_t kNeg136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};  // bf16 -136
-  const u32x4_t kZero = {0u, 0u, 0u, 0u};
 
-  u32x4_t wb[UB][RT], xb[UB][4];
-  auto issue = [&](int u, int c) {
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) wb[u][rt] = wp[rt][4 * c];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) xb[u][s] = xok ? xp[16 * c + s] : kZero;
-  };
-#pragma unroll
-  for (int u = 0; u < UB; ++u)
-    if (c0 + u < c1) issue(u, c0 + u);
-
+  // Batches of UB chunks: all loads of a batch are issued back to back, then the chunks are
+  // consumed in issue order, each waiting only for its own loads. The body has no branches:
+  // chunk indices past the wave's range are clamped to its last chunk (valid memory) and read
+  // the all-zero scale row, so they add nothing. Nothing is carried across batches.
+  const int clast = c1 - 1;
   for (int cb = c0; cb < c1; cb += UB) {
+    u32x4_t wb[UB][RT], xb[UB][4];
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+      const int c = min(cb + u, clast);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) wb[u][rt] = wp[rt][4 * c];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xb[u][s] = xp[16 * c + s];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before any math
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
       const int c = cb + u;
-      if (c < c1) {
-        u32x4_t wc[RT], xc[4];
+      const int g = c < c1 ? c / cpg : KG;
+      // -136 * sum_k x over the chunk, shared by every row tile.
+      f32x4_t corr = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) wc[rt] = wb[u][rt];
+      for (int s = 0; s < 4; ++s)
+        corr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kNeg136), as_bf16x8(xb[u][s]),
+                                                       corr, 0, 0, 0);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) xc[s] = xb[u][s];
-        if (c + UB < c1) issue(u, c + UB);
-
-        // -136 * sum_k x over the chunk, shared by every row tile.
-        f32x4_t corr = {0.f, 0.f, 0.f, 0.f};
+      for (int rt = 0; rt < RT; ++rt) {
+        f32x4_t t = corr;
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          corr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kNeg136), as_bf16x8(xc[s]),
-                                                         corr, 0, 0, 0);
-        const int g = c / cpg;
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          f32x4_t t = corr;
-#pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            uint32_t d[4];
-            unpack_word_128q(wc[rt][s], d);
-            const u32x4_t a = {d[0], d[1], d[2], d[3]};
-            t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(xc[s]), t, 0, 0,
-                                                        0);
-          }
-          // t[r] = partial for row 16 rt + 4 h + r, batch row r16.
-          const uint2 sv = *reinterpret_cast<const uint2*>(&sl[g * ROWS + 16 * rt + 4 * h]);
-          acc[rt][0] = __builtin_fmaf(bf16_bits_to_f32(sv.x & 0xffffu), t[0], acc[rt][0]);
-          acc[rt][1] = __builtin_fmaf(bf16_bits_to_f32(sv.x >> 16), t[1], acc[rt][1]);
-          acc[rt][2] = __builtin_fmaf(bf16_bits_to_f32(sv.y & 0xffffu), t[2], acc[rt][2]);
-          acc[rt][3] = __builtin_fmaf(bf16_bits_to_f32(sv.y >> 16), t[3], acc[rt][3]);
+        for (int s = 0; s < 4; ++s) {
+          uint32_t d[4];
+          unpack_word_128q(wb[u][rt][s], d);
+          const u32x4_t a = {d[0], d[1], d[2], d[3]};
+          t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(xb[u][s]), t, 0, 0, 0);
         }
+        // t[r] = partial for row 16 rt + 4 h + r, batch row r16.
+        const uint2 sv = *reinterpret_cast<const uint2*>(&sl[g * ROWS + 16 * rt + 4 * h]);
+        acc[rt][0] = __builtin_fmaf(bf16_bits_to_f32(sv.x & 0xffffu), t[0], acc[rt][0]);
+        acc[rt][1] = __builtin_fmaf(bf16_bits_to_f32(sv.x >> 16), t[1], acc[rt][1]);
+        acc[rt][2] = __builtin_fmaf(bf16_bits_to_f32(sv.y & 0xffffu), t[2], acc[rt][2]);
+        acc[rt][3] = __builtin_fmaf(bf16_bits_to_f32(sv.y >> 16), t[3], acc[rt][3]);
       }
     }
   }
@@ -178,7 +175,7 @@ __global__ __launch_bounds__(256) void w4_gemv_generic_kernel(
 template <int RT, int NW, int UB>
 hipError_t launch_mfma(const GemvArgs& a, hipStream_t st) {
   const int KG = a.K / a.G;
-  const size_t lds = (size_t)((KG * 16 * RT * 2 + 15) & ~15) + (size_t)NW * RT * 4 * kWave * 4;
+  const size_t lds = (size_t)(((KG + 1) * 16 * RT * 2 + 15) & ~15) + (size_t)NW * RT * 4 * kWave * 4;
   const dim3 grid((a.N + 16 * RT - 1) / (16 * RT));
   hipLaunchKernelGGL((w4_gemv_mfma_kernel<RT, NW, UB>), grid, dim3(NW * kWave), lds, st, a.X,
                      a.Wq, a.S, a.Y, a.M, a.N, a.K, a.G);
@@ -190,7 +187,7 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st) {
 // Scale staging must fit comfortably in LDS next to the reduction buffer.
 bool gemv_fast_path_ok(int M, int N, int K, int G) {
   (void)N;
-  return M >= 1 && M <= 8 && K % 128 == 0 && G % 128 == 0 && (K / G) * 32 * 2 <= 32768;
+  return M >= 1 && M <= 8 && K % 128 == 0 && G % 128 == 0 && (K / G + 1) * 32 * 2 <= 32768;
 }
 
 GemvPlan gemv_plan(int M, int N, int K, int G) {
