@@ -140,6 +140,254 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_mfma_kernel(
   }
 }
 
+// Activations-in-LDS kernel, used whenever M x K bf16 fits in LDS (every M = 1 shape, and
+// M = 8 up to K of about 7000). Same arithmetic as w4_gemv_mfma_kernel, organised to keep the
+// VALU work per weight near one instruction:
+//  * Weights come through buffer loads (one 16-byte load per lane per chunk and row tile):
+//    the per-lane row offset is computed once, the chunk offset is a scalar, and rows past N
+//    read as zero through the buffer's range check, so no address or clamp math per chunk.
+//  * Nibbles are paired (i, i + 4): dword i = bf16(128 + q[i]) | bf16(128 + q[i+4]) << 16 is
+//    one shift and one v_and_or_b32 (mask in a VGPR, exponent bits in an SGPR). X is staged in
+//    LDS with the same pairing (k order 0,4,1,5,2,6,3,7 inside every 8), so both MFMA
+//    operands agree on k.
+//  * The -136 * sum_k x offsets are computed once per wave for all of its chunks, 16 / Mp
+//    chunks per MFMA group (B column j = (batch row j % Mp, chunk j / Mp), A = -136), kept in
+//    LDS, and enter each chunk's product as the MFMA accumulator's initial value.
+//  * Scales are staged in LDS as fp32, transposed to [group][row]: a lane reads its four
+//    rows' scales with one 16-byte LDS read.
+//  * Weights stream through two fixed register sets of UB chunks (double buffering): one set
+//    is in flight while the other is consumed, and a set is refilled only after its last use.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t vmask, uint32_t sbits) {
+  uint32_t d;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(vmask), "s"(sbits));
+  return d;
+}
+
+// Packed word (nibbles k = 0..7) -> four bf16x2 dwords (128 + q[i], 128 + q[i + 4]), i = 0..3.
+__device__ __forceinline__ u32x4_t unpack_word_paired(uint32_t w, uint32_t vmask, uint32_t sbits) {
+  u32x4_t d;
+  d[0] = and_or(w, vmask, sbits);
+  d[1] = and_or(w >> 4, vmask, sbits);
+  d[2] = and_or(w >> 8, vmask, sbits);
+  d[3] = and_or(w >> 12, vmask, sbits);
+  return d;
+}
+
+// Eight bf16 in natural order (4 dwords) -> the same eight in pair order (0,4),(1,5),(2,6),(3,7).
+__device__ __forceinline__ u32x4_t pair_order(const u32x4_t& v) {
+  u32x4_t o;
+  o[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+  o[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+  o[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+  o[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+  return o;
+}
+
+// Chunk bookkeeping of the LDS-activation kernel: every wave runs the same, even number of
+// batches (nbw) of UB chunks per row tile, over a chunk range padded to CP = NW * nbw * UB >= C.
+// LDS tables are padded with zeros up to CP, so the loop has no per-chunk clamps, divisions
+// or branches.
+struct XldsGeom {
+  int nbw, cp;
+};
+__host__ __device__ inline XldsGeom xlds_geom(int K, int nw, int ub) {
+  const int C = K >> 7;
+  const int nbw = 2 * ((C + 2 * nw * ub - 1) / (2 * nw * ub));
+  return XldsGeom{nbw, nw * nbw * ub};
+}
+
+// Persistent workgroups: X (pair order) and the per-chunk offsets are staged once per
+// workgroup, then the workgroup walks row tiles t = blockIdx.x, + gridDim.x, ... Each wave
+// owns a fixed slice of K (split-K inside the workgroup); its weight stream runs through the
+// tiles without a break: the batch after a tile's last one is the next tile's first, and the
+// next tile's scales are loaded during the current tile. One barrier per tile publishes the
+// split-K partials; wave (i % NW) finishes tile i.
+//
+// MFMA roles: A = X (row i = batch row m), B = W^T (column j = output row n), so the result
+// D[m][n] sits in lane (n = lane % 16, m = 4 (lane / 16) + r): each lane needs one scale per
+// chunk, its own row's. Those come from one buffer load per tile (the wave's NCW <= 8 SL
+// consecutive groups of the lane's row) into a wave-private LDS slab. Loads for padded chunks
+// and for tiles past the end use out-of-range buffer offsets: they return zero and touch no
+// memory.
+template <int RT, int NW, int UB, int SL>
+__global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
+    const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
+    const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int M, int N, int K, int G) {
+  constexpr int ROWS = 16 * RT;
+  constexpr uint32_t kOOB = 0x7fffffc0u;  // buffer offset past any range: reads return zero
+  extern __shared__ __align__(16) unsigned char smem[];
+  (void)G;  // this kernel requires G == 128: one scale per chunk
+  const XldsGeom geo = xlds_geom(K, NW, UB);
+  const int KG = K >> 7, C = K >> 7, CP = geo.cp, XP = 128 * CP + 8, KV = K >> 3;
+  const int nbw = geo.nbw, NCW = nbw * UB;  // chunks per wave per tile
+  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                  // [M][128 CP + 8], pair order
+  size_t off = ((size_t)M * XP * 2 + 15) & ~(size_t)15;
+  float* xs = reinterpret_cast<float*>(smem + off);                   // [CP][16]
+  off += (size_t)CP * 16 * 4;
+  uint32_t* slab = reinterpret_cast<uint32_t*>(smem + off);           // [NW][RT][16][4 SL] bf16x2
+  off += (size_t)NW * RT * 16 * 4 * SL * 4;
+  float* red = reinterpret_cast<float*>(smem + off);                  // [2][NW][RT][4][64]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, h = lane >> 4;
+  const int c0 = wv * NCW;
+  const int ntiles = (N + ROWS - 1) / ROWS;
+  const int tstep = gridDim.x;
+
+  // Weight rows through a buffer resource: rows >= N read as zero (range check).
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(Wq), (short)0, (int)((size_t)N * (K >> 1)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(S), (short)0, (int)((size_t)N * KG * 2), 0x00020000);
+  const uint32_t rowb = (uint32_t)(K >> 1);
+  auto issue = [&](u32x4_t (&w)[UB][RT], int tile, int batch) {
+    const bool live = tile < ntiles;
+    const uint32_t vb = (uint32_t)(min(tile, ntiles - 1) * ROWS + r16) * rowb + 16u * h;
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+      const int c = c0 + batch * UB + u;
+      const uint32_t so = (live && c < C) ? 64u * c : kOOB;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+        w[u][rt] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   wres, vb + 16u * rt * rowb, so, 0));
+    }
+  };
+  // Scales of a tile: lane (r16, h == rt) loads groups c0 .. c0 + 8 SL - 1 of row 16 rt + r16.
+  auto load_scales = [&](u32x4_t (&sv)[SL], int tile) {
+    const int rt = min(h, RT - 1);
+    const bool live = tile < ntiles;
+    const uint32_t vb = ((uint32_t)(min(tile, ntiles - 1) * ROWS + 16 * rt + r16) * (uint32_t)KG + c0) * 2u;
+#pragma unroll
+    for (int j = 0; j < SL; ++j)
+      sv[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                              sres, vb, live ? 16u * j : kOOB, 0));
+  };
+  uint32_t* wslab = slab + wv * RT * 16 * 4 * SL;
+  auto store_scales = [&](const u32x4_t (&sv)[SL]) {
+    if (h < RT) {
+#pragma unroll
+      for (int j = 0; j < SL; ++j)
+        *reinterpret_cast<u32x4_t*>(&wslab[(h * 16 + r16) * 4 * SL + 4 * j]) = sv[j];
+    }
+  };
+
+  int tile = blockIdx.x;
+  // The first weight batch is in flight while X is staged and the offsets are computed.
+  u32x4_t wa[UB][RT], wb[UB][RT];
+  u32x4_t sv[SL];
+  issue(wa, tile, 0);
+  load_scales(sv, tile);
+  __builtin_amdgcn_sched_barrier(0);
+
+  const u32x4_t* x4 = reinterpret_cast<const u32x4_t*>(X);
+  const int XV = 16 * CP;  // 8-element pieces per padded row
+  for (int e = tid; e < M * XV; e += NW * kWave) {
+    const int m = e / XV, v = e - m * XV;
+    const u32x4_t val = v < KV ? pair_order(x4[m * KV + v]) : u32x4_t{0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x4_t*>(&xl[m * XP + 8 * v]) = val;
+  }
+  store_scales(sv);
+  __syncthreads();
+
+  // xs[c][m] = -136 * sum_k x[m][k] over chunk c: one MFMA group covers 16 / mp chunks
+  // (B column j = (batch row j % mp, chunk j / mp), A = -136); columns m >= M hold 0.
+  const u32x4_t kNeg136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};  // bf16 -136
+  {
+    const int mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+    const int per = 16 / mp;
+    const int mj = min(r16 % mp, M - 1), cc = r16 / mp;
+    for (int cg = c0; cg < c0 + NCW; cg += per) {
+      const int c = min(cg + cc, CP - 1);
+      const uint16_t* xr = &xl[mj * XP + 128 * c + 32 * h];
+      f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(kNeg136), as_bf16x8(*reinterpret_cast<const u32x4_t*>(xr + 8 * s)), d, 0, 0, 0);
+      if (h == 0) {
+        const int m = r16 % mp;
+        if (cg + cc < CP) {
+          xs[(cg + cc) * 16 + m] = m < M ? d[0] : 0.f;
+          if (m == mp - 1)
+            for (int z = mp; z < 16; ++z) xs[(cg + cc) * 16 + z] = 0.f;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  uint32_t vmask;
+  asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(vmask));
+  const uint32_t sbits = 0x43004300u;  // bf16 exponent of 128 in both halves
+  const int mx = min(r16, M - 1);
+  const uint16_t* xl_l = xl + mx * XP + 32 * h;
+  const float* xs_l = xs + 4 * h;
+  const uint16_t* sl_l = reinterpret_cast<const uint16_t*>(wslab) + r16 * 8 * SL;
+  f32x4_t acc[RT];
+
+  auto compute = [&](const u32x4_t (&w)[UB][RT], int batch) {
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+      const int cw = batch * UB + u, c = c0 + cw;
+      const f32x4_t init = *reinterpret_cast<const f32x4_t*>(xs_l + c * 16);
+      u32x4_t xb[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) xb[s] = *reinterpret_cast<const u32x4_t*>(xl_l + 128 * c + 8 * s);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        f32x4_t t = init;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              as_bf16x8(xb[s]), as_bf16x8(unpack_word_paired(w[u][rt][s], vmask, sbits)), t, 0, 0, 0);
+        const float sc = bf16_bits_to_f32(sl_l[rt * 16 * 8 * SL + cw]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[rt][r] = __builtin_fmaf(sc, t[r], acc[rt][r]);
+      }
+    }
+  };
+
+  for (int it = 0; tile < ntiles; ++it, tile += tstep) {
+    const int tnext = tile + tstep;  // may be past the end: its loads are out of range
+    load_scales(sv, tnext);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < nbw; b += 2) {
+      issue(wb, tile, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(wa, b);
+      __builtin_amdgcn_sched_barrier(0);
+      const bool last = b + 2 >= nbw;
+      issue(wa, last ? tnext : tile, last ? 0 : b + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(wb, b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    float* rd = red + (it & 1) * NW * RT * 4 * kWave;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rd[((wv * RT + rt) * 4 + r) * kWave + lane] = acc[rt][r];
+    store_scales(sv);  // wave-private; its last reader was the compute above
+    __syncthreads();
+    if (wv == it % NW) {
+      const int n0 = tile * ROWS;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = 0.f;
+#pragma unroll
+          for (int w = 0; w < NW; ++w) v += rd[((w * RT + rt) * 4 + r) * kWave + lane];
+          const int m = 4 * h + r, n = n0 + 16 * rt + r16;
+          if (m < M && n < N) Y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v);
+        }
+    }
+  }
+}
+
 // Generic fallback: one wavefront per output row, exact fp32 dequant, fp32 FMA.
 template <int MMAX>
 __global__ __launch_bounds__(256) void w4_gemv_generic_kernel(
@@ -182,9 +430,46 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st) {
   return hipSuccess;
 }
 
+size_t xlds_bytes(int M, int K, int G, int rt, int nw, int ub, int sl) {
+  (void)G;
+  const XldsGeom geo = xlds_geom(K, nw, ub);
+  const size_t a = ((size_t)M * (128 * geo.cp + 8) * 2 + 15) & ~(size_t)15;
+  return a + (size_t)geo.cp * 16 * 4 + (size_t)nw * rt * 16 * 4 * sl * 4 +
+         (size_t)2 * nw * rt * 4 * kWave * 4;
+}
+
+// Smallest scale-slab size (in 16-byte loads per lane) covering a wave's chunks; 0 if none.
+int xlds_sl(int K, int G, int rt, int nw, int ub) {
+  if (G != 128 || rt > 4 || (K / G) % 2) return 0;  // dword-aligned scale loads need even K/G
+  const XldsGeom geo = xlds_geom(K, nw, ub);
+  const int ncw = geo.nbw * ub;
+  return ncw <= 8 ? 1 : ncw <= 16 ? 2 : ncw <= 32 ? 4 : 0;
+}
+
+template <int RT, int NW, int UB, int SL>
+hipError_t launch_xlds(const GemvArgs& a, hipStream_t st) {
+  const void* fn = reinterpret_cast<const void*>(&w4_gemv_xlds_kernel<RT, NW, UB, SL>);
+  // Opt in once per instantiation to LDS beyond 64 KiB (gfx950 has 160 KiB per CU).
+  static const hipError_t attr =
+      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (attr != hipSuccess) return attr;
+  const size_t lds = xlds_bytes(a.M, a.K, a.G, RT, NW, UB, SL);
+  int per_cu = 0;
+  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NW * kWave, lds);
+  if (e != hipSuccess) return e;
+  int cus = 0;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+  if (e != hipSuccess) return e;
+  const int ntiles = (a.N + 16 * RT - 1) / (16 * RT);
+  const int grid = max(1, min(ntiles, max(per_cu, 1) * cus));
+  hipLaunchKernelGGL((w4_gemv_xlds_kernel<RT, NW, UB, SL>), dim3(grid), dim3(NW * kWave), lds, st,
+                     a.X, a.Wq, a.S, a.Y, a.M, a.N, a.K, a.G);
+  return hipSuccess;
+}
+
 }  // namespace
 
-// Scale staging must fit comfortably in LDS next to the reduction buffer.
+// Register-X kernel limits: scale staging must fit comfortably in LDS next to the reduction.
 bool gemv_fast_path_ok(int M, int N, int K, int G) {
   (void)N;
   return M >= 1 && M <= 8 && K % 128 == 0 && G % 128 == 0 && (K / G + 1) * 32 * 2 <= 32768;
@@ -195,15 +480,21 @@ GemvPlan gemv_plan(int M, int N, int K, int G) {
   p.fast = gemv_fast_path_ok(M, N, K, G);
   if (!p.fast) return p;
   const int C = K / 128;
-  const int tiles1 = (N + 15) / 16;
-  // Row tiles of 32 when there are plenty of rows (halves the X traffic per weight byte),
-  // then split K over enough waves that the chip holds >= ~2048 waves, keeping >= 2 chunks
-  // per wave.
-  p.rt = tiles1 >= 2048 ? 2 : 1;
-  const int tiles = (N + 16 * p.rt - 1) / (16 * p.rt);
-  int nw = 1;
-  while (nw < 8 && (long)tiles * nw < 2048 && C / (2 * nw) >= 2) nw *= 2;
-  p.nw = nw;
+  // LDS-activation kernel when X fits and the weight bytes fit a 31-bit buffer offset.
+  const bool small_buf = (size_t)N * (K / 2) + (size_t)16 * K < ((size_t)1 << 31);
+  p.rt = 1;
+  p.nw = N >= 16384 ? 4 : 8;
+  while (p.nw > 1 && C / p.nw < 2) p.nw /= 2;
+  p.sl = xlds_sl(K, G, p.rt, p.nw, 2);
+  p.xlds = small_buf && p.sl > 0 && xlds_bytes(M, K, G, p.rt, p.nw, 2, p.sl) <= 96 * 1024;
+  if (!p.xlds) {
+    const int tiles1 = (N + 15) / 16;
+    p.rt = tiles1 >= 2048 ? 2 : 1;
+    const int tiles = (N + 16 * p.rt - 1) / (16 * p.rt);
+    int nw = 1;
+    while (nw < 8 && (long)tiles * nw < 2048 && C / (2 * nw) >= 2) nw *= 2;
+    p.nw = nw;
+  }
   return p;
 }
 
@@ -212,6 +503,16 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
     hipLaunchKernelGGL((w4_gemv_generic_kernel<8>), dim3((a.N + 3) / 4), dim3(256), 0, st, a.X,
                        a.Wq, a.S, a.Y, a.M, a.N, a.K, a.G);
     return hipSuccess;
+  }
+  if (p.xlds) {
+#define NS_XLDS_CASE(NW_, SL_) \
+  if (p.rt == 1 && p.nw == NW_ && p.sl == SL_) return launch_xlds<1, NW_, 2, SL_>(a, st);
+    NS_XLDS_CASE(1, 1) NS_XLDS_CASE(1, 2) NS_XLDS_CASE(1, 4)
+    NS_XLDS_CASE(2, 1) NS_XLDS_CASE(2, 2) NS_XLDS_CASE(2, 4)
+    NS_XLDS_CASE(4, 1) NS_XLDS_CASE(4, 2) NS_XLDS_CASE(4, 4)
+    NS_XLDS_CASE(8, 1) NS_XLDS_CASE(8, 2) NS_XLDS_CASE(8, 4)
+#undef NS_XLDS_CASE
+    return hipErrorInvalidValue;
   }
 #define NS_GEMV_CASE(RT_, NW_)                                   \
   if (p.rt == RT_ && p.nw == NW_) return launch_mfma<RT_, NW_, 4>(a, st);

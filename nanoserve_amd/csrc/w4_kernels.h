@@ -14,9 +14,11 @@ struct GemvArgs {
 };
 
 struct GemvPlan {
-  bool fast;  // MFMA kernel (K % 128 == 0, G % 128 == 0); otherwise the generic kernel
+  bool fast;  // MFMA kernels (K % 128 == 0, G % 128 == 0); otherwise the generic kernel
+  bool xlds;  // activations staged in LDS (w4_gemv_xlds_kernel); otherwise in registers
   int rt;     // 16-row tiles per wavefront
   int nw;     // wavefronts per workgroup splitting K
+  int sl;     // scale slab loads per lane per tile (LDS-activation kernel)
 };
 
 bool gemv_fast_path_ok(int M, int N, int K, int G);
