@@ -183,17 +183,16 @@ __device__ __forceinline__ u32x4_t pair_order(const u32x4_t& v) {
   return o;
 }
 
-// Chunk bookkeeping of the LDS-activation kernel: every wave runs the same, even number of
-// batches (nbw) of UB chunks per row tile, over a chunk range padded to CP = NW * nbw * UB >= C.
-// LDS tables are padded with zeros up to CP, so the loop has no per-chunk clamps, divisions
-// or branches.
+// Chunk bookkeeping of the LDS-activation kernel: every wave owns NCW chunks of each row tile,
+// a multiple of the ring depth R, over a chunk range padded to CP = NW * NCW >= C. LDS tables
+// are padded with zeros up to CP, so the loop has no per-chunk clamps, divisions or branches.
 struct XldsGeom {
-  int nbw, cp;
+  int ncw, cp;
 };
-__host__ __device__ inline XldsGeom xlds_geom(int K, int nw, int ub) {
+__host__ __device__ inline XldsGeom xlds_geom(int K, int nw, int r) {
   const int C = K >> 7;
-  const int nbw = 2 * ((C + 2 * nw * ub - 1) / (2 * nw * ub));
-  return XldsGeom{nbw, nw * nbw * ub};
+  const int ncw = r * ((C + nw * r - 1) / (nw * r));
+  return XldsGeom{ncw, nw * ncw};
 }
 
 // Persistent workgroups: X (pair order) and the per-chunk offsets are staged once per
@@ -203,13 +202,17 @@ __host__ __device__ inline XldsGeom xlds_geom(int K, int nw, int ub) {
 // next tile's scales are loaded during the current tile. One barrier per tile publishes the
 // split-K partials; wave (i % NW) finishes tile i.
 //
+// Weights stream through a ring of R register slots (one chunk of RT row tiles each): a slot
+// is consumed, then immediately refilled with the chunk R positions ahead in the wave's stream
+// (continuing into the next tile), so R - 1 chunks are always in flight per wave.
+//
 // MFMA roles: A = X (row i = batch row m), B = W^T (column j = output row n), so the result
 // D[m][n] sits in lane (n = lane % 16, m = 4 (lane / 16) + r): each lane needs one scale per
 // chunk, its own row's. Those come from one buffer load per tile (the wave's NCW <= 8 SL
 // consecutive groups of the lane's row) into a wave-private LDS slab. Loads for padded chunks
 // and for tiles past the end use out-of-range buffer offsets: they return zero and touch no
 // memory.
-template <int RT, int NW, int UB, int SL>
+template <int RT, int NW, int R, int SL>
 __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
     const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
     const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int M, int N, int K, int G) {
@@ -217,9 +220,9 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
   constexpr uint32_t kOOB = 0x7fffffc0u;  // buffer offset past any range: reads return zero
   extern __shared__ __align__(16) unsigned char smem[];
   (void)G;  // this kernel requires G == 128: one scale per chunk
-  const XldsGeom geo = xlds_geom(K, NW, UB);
+  const XldsGeom geo = xlds_geom(K, NW, R);
   const int KG = K >> 7, C = K >> 7, CP = geo.cp, XP = 128 * CP + 8, KV = K >> 3;
-  const int nbw = geo.nbw, NCW = nbw * UB;  // chunks per wave per tile
+  const int NCW = geo.ncw;  // chunks per wave per tile, a multiple of R
   uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                  // [M][128 CP + 8], pair order
   size_t off = ((size_t)M * XP * 2 + 15) & ~(size_t)15;
   float* xs = reinterpret_cast<float*>(smem + off);                   // [CP][16]
@@ -241,18 +244,15 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
   const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(S), (short)0, (int)((size_t)N * KG * 2), 0x00020000);
   const uint32_t rowb = (uint32_t)(K >> 1);
-  auto issue = [&](u32x4_t (&w)[UB][RT], int tile, int batch) {
+  auto issue = [&](u32x4_t (&w)[RT], int tile, int cw) {
     const bool live = tile < ntiles;
     const uint32_t vb = (uint32_t)(min(tile, ntiles - 1) * ROWS + r16) * rowb + 16u * h;
+    const int c = c0 + cw;
+    const uint32_t so = (live && c < C) ? 64u * c : kOOB;
 #pragma unroll
-    for (int u = 0; u < UB; ++u) {
-      const int c = c0 + batch * UB + u;
-      const uint32_t so = (live && c < C) ? 64u * c : kOOB;
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt)
-        w[u][rt] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   wres, vb + 16u * rt * rowb, so, 0));
-    }
+    for (int rt = 0; rt < RT; ++rt)
+      w[rt] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                              wres, vb + 16u * rt * rowb, so, 0));
   };
   // Scales of a tile: lane (r16, h == rt) loads groups c0 .. c0 + 8 SL - 1 of row 16 rt + r16.
   auto load_scales = [&](u32x4_t (&sv)[SL], int tile) {
@@ -274,10 +274,11 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
   };
 
   int tile = blockIdx.x;
-  // The first weight batch is in flight while X is staged and the offsets are computed.
-  u32x4_t wa[UB][RT], wb[UB][RT];
+  // The first R chunks are in flight while X is staged and the offsets are computed.
+  u32x4_t ring[R][RT];
   u32x4_t sv[SL];
-  issue(wa, tile, 0);
+#pragma unroll
+  for (int u = 0; u < R; ++u) issue(ring[u], tile, u);
   load_scales(sv, tile);
   __builtin_amdgcn_sched_barrier(0);
 
@@ -327,25 +328,22 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
   const uint16_t* sl_l = reinterpret_cast<const uint16_t*>(wslab) + r16 * 8 * SL;
   f32x4_t acc[RT];
 
-  auto compute = [&](const u32x4_t (&w)[UB][RT], int batch) {
+  auto compute = [&](const u32x4_t (&w)[RT], int cw) {
+    const int c = c0 + cw;
+    const f32x4_t init = *reinterpret_cast<const f32x4_t*>(xs_l + c * 16);
+    u32x4_t xb[4];
 #pragma unroll
-    for (int u = 0; u < UB; ++u) {
-      const int cw = batch * UB + u, c = c0 + cw;
-      const f32x4_t init = *reinterpret_cast<const f32x4_t*>(xs_l + c * 16);
-      u32x4_t xb[4];
+    for (int s = 0; s < 4; ++s) xb[s] = *reinterpret_cast<const u32x4_t*>(xl_l + 128 * c + 8 * s);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) xb[s] = *reinterpret_cast<const u32x4_t*>(xl_l + 128 * c + 8 * s);
+    for (int rt = 0; rt < RT; ++rt) {
+      f32x4_t t = init;
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        f32x4_t t = init;
+      for (int s = 0; s < 4; ++s)
+        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(xb[s]), as_bf16x8(unpack_word_paired(w[rt][s], vmask, sbits)), t, 0, 0, 0);
+      const float sc = bf16_bits_to_f32(sl_l[rt * 16 * 8 * SL + cw]);
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              as_bf16x8(xb[s]), as_bf16x8(unpack_word_paired(w[u][rt][s], vmask, sbits)), t, 0, 0, 0);
-        const float sc = bf16_bits_to_f32(sl_l[rt * 16 * 8 * SL + cw]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[rt][r] = __builtin_fmaf(sc, t[r], acc[rt][r]);
-      }
+      for (int r = 0; r < 4; ++r) acc[rt][r] = __builtin_fmaf(sc, t[r], acc[rt][r]);
     }
   };
 
@@ -354,16 +352,15 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
     load_scales(sv, tnext);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    for (int b = 0; b < nbw; b += 2) {
-      issue(wb, tile, b + 1);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(wa, b);
-      __builtin_amdgcn_sched_barrier(0);
-      const bool last = b + 2 >= nbw;
-      issue(wa, last ? tnext : tile, last ? 0 : b + 2);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(wb, b + 1);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int j = 0; j < NCW; j += R) {
+      const bool last = j + R >= NCW;  // refills of this pass go to the next tile
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+        compute(ring[u], j + u);
+        __builtin_amdgcn_sched_barrier(0);
+        issue(ring[u], last ? tnext : tile, last ? u : j + R + u);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     float* rd = red + (it & 1) * NW * RT * 4 * kWave;
 #pragma unroll
@@ -386,6 +383,144 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
         }
     }
   }
+}
+
+// M = 1 streaming kernel ("diagonal" MFMA). The packed weights are read as one contiguous
+// stream: every wave instruction loads 1 KiB = 16 consecutive 64-byte pieces, and with
+// G = 128 and K % 128 == 0 a piece is exactly one scale group (128 k) of one row. Lane
+// l = 16 kg + j holds 16 bytes (words 4 kg .. 4 kg + 3) of piece j.
+//  * MFMA roles: A row j = the X slice matching piece j (from LDS, per lane), B column j =
+//    piece j. The diagonal D[j][j] = sum over the piece of x * (128 + q) is the piece's partial
+//    dot product; off-diagonal entries are cross terms and are discarded. Per 2048 weights
+//    this is the same four MFMAs as the row-tiled kernel, but HBM sees a purely sequential
+//    stream.
+//  * The accumulator starts at -136 * sum(x over the piece's k range) (per-chunk table xs in
+//    LDS), so D[j][j] = sum x * (q - 8) exactly as in the reference dequant.
+//  * The piece's scale is S[flat piece index] (S is [N][K / 128], i.e. one bf16 per piece in
+//    the same order): 16 consecutive bf16 per block, one 2-byte buffer load per lane.
+//  * Workgroups are persistent over 16-row groups; the C = K / 128 blocks of a group are dealt
+//    to the NW waves round-robin. Each diagonal lane writes scale * D[j][j] to an LDS partial
+//    table (double-buffered by group parity); after the group's barrier, 16 lanes per row sum
+//    the row's C partials and wave (i % NW) writes Y.
+//  * Blocks stream through a ring of R register slots (R - 1 blocks in flight per wave),
+//    continuing across row groups.
+template <int NW, int R>
+__global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
+    const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
+    const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int N, int K) {
+  constexpr uint32_t kOOB = 0x7fffffc0u;  // buffer offset past any range: reads return zero
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int C = K >> 7, KV = K >> 3;
+  const int CP = (C + 15) & ~15;                                       // padded for the xs pass
+  // X in LDS, pair order, one 128-element chunk per 136-element row: the 16-byte row padding
+  // puts the 16 lanes that read 16 different chunks on 16 different bank groups.
+  constexpr int XR = 136;
+  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                    // [CP][136]
+  float* xs = reinterpret_cast<float*>(smem + (size_t)CP * XR * 2);    // [CP]
+  float* part = xs + CP;                                               // [2][16 C]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15, kg = lane >> 4;
+  const int ngroups = (N + 15) >> 4;
+  const int gstep = gridDim.x;
+  // Every wave runs nbp block slots per group (a multiple of R); wave wv's slot i is block
+  // b = wv + NW i of the group, and slots with b >= C are padding (no memory traffic).
+  const int nbp = R * ((C + NW * R - 1) / (NW * R));
+
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(Wq), (short)0, (int)((size_t)N * (K >> 1)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(S), (short)0, (int)((size_t)N * C * 2), 0x00020000);
+  const uint32_t vw = 64u * j + 16u * kg;  // this lane's bytes inside a 1 KiB block
+  const uint32_t vs = 2u * j;              // this lane's scale among a block's 16
+
+  // Block (g, b) covers the group's pieces 16 b .. 16 b + 15, i.e. flat block g C + b.
+  auto issue = [&](u32x4_t& w, uint32_t& sc, int g, int i) {
+    const int b = wv + NW * i;
+    const bool live = g < ngroups && b < C;
+    const uint32_t blk = (uint32_t)(g * C + b);
+    w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                        wres, vw, live ? 1024u * blk : kOOB, 0));
+    sc = __builtin_amdgcn_raw_buffer_load_b16(sres, vs, live ? 32u * blk : kOOB, 0);
+  };
+
+  int g = blockIdx.x;
+  // The first R slots are in flight while X is staged.
+  u32x4_t ring[R];
+  uint32_t rsc[R];
+#pragma unroll
+  for (int u = 0; u < R; ++u) issue(ring[u], rsc[u], g, u);
+  __builtin_amdgcn_sched_barrier(0);
+
+  const u32x4_t* x4 = reinterpret_cast<const u32x4_t*>(X);
+  for (int e = tid; e < 16 * CP; e += NW * kWave)
+    *reinterpret_cast<u32x4_t*>(&xl[(e >> 4) * XR + 8 * (e & 15)]) =
+        e < KV ? pair_order(x4[e]) : u32x4_t{0u, 0u, 0u, 0u};
+  __syncthreads();
+  // xs[c] = -136 * sum of x over chunk c: MFMA with A = -136, B column j = chunk cg + j.
+  const u32x4_t kNeg136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
+  for (int cg = 16 * wv; cg < CP; cg += 16 * NW) {
+    const uint16_t* xr = &xl[XR * (cg + j) + 32 * kg];
+    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          as_bf16x8(kNeg136), as_bf16x8(*reinterpret_cast<const u32x4_t*>(xr + 8 * s4)), d, 0, 0, 0);
+    if (kg == 0) xs[cg + j] = d[0];
+  }
+  __syncthreads();
+
+  uint32_t vmask;
+  asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(vmask));
+  const uint32_t sbits = 0x43004300u;
+  const bool diag = kg == (j >> 2);  // this lane holds D[j][j], in register j % 4
+  const int dr = j & 3;
+  // Chunk of piece j of slot i: (16 (wv + NW i) + j) % C, advanced incrementally.
+  const int c_first = (16 * wv + j) % C;
+  const int c_step = (16 * NW) % C;
+  for (int it = 0; g < ngroups; ++it, g += gstep) {
+    float* pt = part + (it & 1) * 16 * C;
+    int c = c_first;
+    for (int i0 = 0; i0 < nbp; i0 += R) {
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+        const int b = wv + NW * (i0 + u);
+        const f32x4_t init = {xs[c], xs[c], xs[c], xs[c]};
+        const uint16_t* xr = &xl[XR * c + 32 * kg];
+        f32x4_t t = init;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+          t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              as_bf16x8(*reinterpret_cast<const u32x4_t*>(xr + 8 * s4)),
+              as_bf16x8(unpack_word_paired(ring[u][s4], vmask, sbits)), t, 0, 0, 0);
+        const float v = dr == 0 ? t[0] : dr == 1 ? t[1] : dr == 2 ? t[2] : t[3];
+        if (b < C && diag) pt[16 * b + j] = bf16_bits_to_f32(rsc[u] & 0xffffu) * v;
+        c += c_step;
+        c = c >= C ? c - C : c;
+        __builtin_amdgcn_sched_barrier(0);
+        // Refill: slot i0 + u + R of this group, or slot i0 + u + R - nbp of the next group.
+        const bool wrap = i0 + R >= nbp;
+        issue(ring[u], rsc[u], wrap ? g + gstep : g, wrap ? u : i0 + R + u);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __syncthreads();
+    if (wv == it % NW) {
+      // Rows of the group: lane (row j, part kg) sums chunks kg, kg + 4, ...; then 4-lane sum.
+      float v = 0.f;
+      for (int cc = kg; cc < C; cc += 4) v += pt[j * C + cc];
+      v += __shfl_xor(v, 16, kWave);
+      v += __shfl_xor(v, 32, kWave);
+      const int n = 16 * g + j;
+      if (kg == 0 && n < N) Y[n] = (uint16_t)f32_to_bf16_rne(v);
+    }
+  }
+}
+
+size_t m1_bytes(int K) {
+  const int C = K >> 7, CP = (C + 15) & ~15;
+  return (size_t)CP * 136 * 2 + (size_t)CP * 4 + (size_t)2 * 16 * C * 4;
 }
 
 // Generic fallback: one wavefront per output row, exact fp32 dequant, fp32 FMA.
@@ -430,30 +565,30 @@ hipError_t launch_mfma(const GemvArgs& a, hipStream_t st) {
   return hipSuccess;
 }
 
-size_t xlds_bytes(int M, int K, int G, int rt, int nw, int ub, int sl) {
+size_t xlds_bytes(int M, int K, int G, int rt, int nw, int r, int sl) {
   (void)G;
-  const XldsGeom geo = xlds_geom(K, nw, ub);
+  const XldsGeom geo = xlds_geom(K, nw, r);
   const size_t a = ((size_t)M * (128 * geo.cp + 8) * 2 + 15) & ~(size_t)15;
   return a + (size_t)geo.cp * 16 * 4 + (size_t)nw * rt * 16 * 4 * sl * 4 +
          (size_t)2 * nw * rt * 4 * kWave * 4;
 }
 
 // Smallest scale-slab size (in 16-byte loads per lane) covering a wave's chunks; 0 if none.
-int xlds_sl(int K, int G, int rt, int nw, int ub) {
+int xlds_sl(int K, int G, int rt, int nw, int r) {
   if (G != 128 || rt > 4 || (K / G) % 2) return 0;  // dword-aligned scale loads need even K/G
-  const XldsGeom geo = xlds_geom(K, nw, ub);
-  const int ncw = geo.nbw * ub;
+  const XldsGeom geo = xlds_geom(K, nw, r);
+  const int ncw = geo.ncw;
   return ncw <= 8 ? 1 : ncw <= 16 ? 2 : ncw <= 32 ? 4 : 0;
 }
 
-template <int RT, int NW, int UB, int SL>
+template <int RT, int NW, int R, int SL>
 hipError_t launch_xlds(const GemvArgs& a, hipStream_t st) {
-  const void* fn = reinterpret_cast<const void*>(&w4_gemv_xlds_kernel<RT, NW, UB, SL>);
+  const void* fn = reinterpret_cast<const void*>(&w4_gemv_xlds_kernel<RT, NW, R, SL>);
   // Opt in once per instantiation to LDS beyond 64 KiB (gfx950 has 160 KiB per CU).
   static const hipError_t attr =
       hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (attr != hipSuccess) return attr;
-  const size_t lds = xlds_bytes(a.M, a.K, a.G, RT, NW, UB, SL);
+  const size_t lds = xlds_bytes(a.M, a.K, a.G, RT, NW, R, SL);
   int per_cu = 0;
   hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NW * kWave, lds);
   if (e != hipSuccess) return e;
@@ -462,9 +597,53 @@ hipError_t launch_xlds(const GemvArgs& a, hipStream_t st) {
   if (e != hipSuccess) return e;
   const int ntiles = (a.N + 16 * RT - 1) / (16 * RT);
   const int grid = max(1, min(ntiles, max(per_cu, 1) * cus));
-  hipLaunchKernelGGL((w4_gemv_xlds_kernel<RT, NW, UB, SL>), dim3(grid), dim3(NW * kWave), lds, st,
+  hipLaunchKernelGGL((w4_gemv_xlds_kernel<RT, NW, R, SL>), dim3(grid), dim3(NW * kWave), lds, st,
                      a.X, a.Wq, a.S, a.Y, a.M, a.N, a.K, a.G);
   return hipSuccess;
+}
+
+template <int NW, int R>
+hipError_t launch_m1(const GemvArgs& a, hipStream_t st) {
+  const void* fn = reinterpret_cast<const void*>(&w4_gemv_m1_kernel<NW, R>);
+  static const hipError_t attr =
+      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (attr != hipSuccess) return attr;
+  const size_t lds = m1_bytes(a.K);
+  int per_cu = 0;
+  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NW * kWave, lds);
+  if (e != hipSuccess) return e;
+  int cus = 0;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+  if (e != hipSuccess) return e;
+  const int ngroups = (a.N + 15) / 16;
+  const int grid = max(1, min(ngroups, max(per_cu, 1) * cus));
+  hipLaunchKernelGGL((w4_gemv_m1_kernel<NW, R>), dim3(grid), dim3(NW * kWave), lds, st, a.X, a.Wq,
+                     a.S, a.Y, a.N, a.K);
+  return hipSuccess;
+}
+
+// (NW, R) for the M = 1 kernel. With fewer 16-row groups than twice the CU count, 14 or 16
+// waves per group (split K further) so every CU keeps enough loads in flight, with the deeper
+// ring once each wave has >= 8 blocks per group; otherwise 7 or 8 waves with a 4-deep ring,
+// whichever pads fewer block slots.
+void m1_choose(int N, int K, int& nw, int& r) {
+  const int C = K >> 7, groups = (N + 15) / 16;
+  auto waste = [&](int n, int rr) {
+    const int nbp = rr * ((C + n * rr - 1) / (n * rr));
+    return n * nbp - C;
+  };
+  if (groups < 512 && C >= 14) {
+    if (C >= 128) {
+      nw = 16;
+      r = 4;
+    } else {
+      r = 2;
+      nw = waste(14, 2) < waste(16, 2) ? 14 : 16;
+    }
+    return;
+  }
+  r = 4;
+  nw = C >= 8 && waste(7, 4) < waste(8, 4) ? 7 : (C >= 8 ? 8 : 3);
 }
 
 }  // namespace
@@ -482,11 +661,16 @@ GemvPlan gemv_plan(int M, int N, int K, int G) {
   const int C = K / 128;
   // LDS-activation kernel when X fits and the weight bytes fit a 31-bit buffer offset.
   const bool small_buf = (size_t)N * (K / 2) + (size_t)16 * K < ((size_t)1 << 31);
+  p.m1 = M == 1 && G == 128 && small_buf && m1_bytes(K) <= 96 * 1024;
+  if (p.m1) {
+    m1_choose(N, K, p.nw, p.rt);
+    return p;
+  }
   p.rt = 1;
   p.nw = N >= 16384 ? 4 : 8;
   while (p.nw > 1 && C / p.nw < 2) p.nw /= 2;
-  p.sl = xlds_sl(K, G, p.rt, p.nw, 2);
-  p.xlds = small_buf && p.sl > 0 && xlds_bytes(M, K, G, p.rt, p.nw, 2, p.sl) <= 96 * 1024;
+  p.sl = xlds_sl(K, G, p.rt, p.nw, 4);
+  p.xlds = small_buf && p.sl > 0 && xlds_bytes(M, K, G, p.rt, p.nw, 4, p.sl) <= 96 * 1024;
   if (!p.xlds) {
     const int tiles1 = (N + 15) / 16;
     p.rt = tiles1 >= 2048 ? 2 : 1;
@@ -504,9 +688,20 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
                        a.Wq, a.S, a.Y, a.M, a.N, a.K, a.G);
     return hipSuccess;
   }
+  if (p.m1) {
+    if (p.nw == 16 && p.rt == 2) return launch_m1<16, 2>(a, st);
+    if (p.nw == 14 && p.rt == 2) return launch_m1<14, 2>(a, st);
+    if (p.nw == 16 && p.rt == 4) return launch_m1<16, 4>(a, st);
+    if (p.nw == 8 && p.rt == 4) return launch_m1<8, 4>(a, st);
+    if (p.nw == 8 && p.rt == 2) return launch_m1<8, 2>(a, st);
+    if (p.nw == 7 && p.rt == 4) return launch_m1<7, 4>(a, st);
+    if (p.nw == 4 && p.rt == 4) return launch_m1<4, 4>(a, st);
+    if (p.nw == 3 && p.rt == 4) return launch_m1<3, 4>(a, st);
+    return hipErrorInvalidValue;
+  }
   if (p.xlds) {
 #define NS_XLDS_CASE(NW_, SL_) \
-  if (p.rt == 1 && p.nw == NW_ && p.sl == SL_) return launch_xlds<1, NW_, 2, SL_>(a, st);
+  if (p.rt == 1 && p.nw == NW_ && p.sl == SL_) return launch_xlds<1, NW_, 4, SL_>(a, st);
     NS_XLDS_CASE(1, 1) NS_XLDS_CASE(1, 2) NS_XLDS_CASE(1, 4)
     NS_XLDS_CASE(2, 1) NS_XLDS_CASE(2, 2) NS_XLDS_CASE(2, 4)
     NS_XLDS_CASE(4, 1) NS_XLDS_CASE(4, 2) NS_XLDS_CASE(4, 4)

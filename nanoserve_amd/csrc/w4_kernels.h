@@ -15,6 +15,7 @@ struct GemvArgs {
 
 struct GemvPlan {
   bool fast;  // MFMA kernels (K % 128 == 0, G % 128 == 0); otherwise the generic kernel
+  bool m1;    // M = 1 streaming kernel (w4_gemv_m1_kernel); rt holds its ring depth
   bool xlds;  // activations staged in LDS (w4_gemv_xlds_kernel); otherwise in registers
   int rt;     // 16-row tiles per wavefront
   int nw;     // wavefronts per workgroup splitting K
