@@ -35,16 +35,27 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) {
 }
 
 // One packed word -> 8 staged weights bf16_rne((q - 8) * s), natural k order, as 4 bf16x2.
-__device__ __forceinline__ u32x4_t dequant_word_bf16(uint32_t w, float s, float ns8) {
-  const uint32_t t0 = w & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6 in bytes 0..3
-  const uint32_t t1 = (w >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
+// The nibbles are isolated into bytes with one mask each (lo: even nibbles, hi: odd nibbles;
+// vmask = 0x0F0F0F0F in a VGPR) and converted by v_cvt_f32_ubyte0..3, which read a byte
+// directly; fma(q, s, -8 s) is (q - 8) s exactly; v_cvt_pk_bf16_f32 rounds to nearest even.
+template <int B>
+__device__ __forceinline__ float cvt_ubyte(uint32_t v) {
+  float f;
+  if (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(v));
+  if (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(v));
+  if (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(v));
+  if (B == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(v));
+  return f;
+}
+
+__device__ __forceinline__ u32x4_t dequant_word_bf16(uint32_t w, uint32_t vmask, float s, float ns8) {
+  const uint32_t t0 = w & vmask;         // nibbles 0, 2, 4, 6 in bytes 0..3
+  const uint32_t t1 = (w >> 4) & vmask;  // nibbles 1, 3, 5, 7
   u32x4_t d;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float lo = (float)((t0 >> (8 * j)) & 0xFFu);
-    const float hi = (float)((t1 >> (8 * j)) & 0xFFu);
-    d[j] = pack_bf16x2_rne(__builtin_fmaf(lo, s, ns8), __builtin_fmaf(hi, s, ns8));
-  }
+  d[0] = pack_bf16x2_rne(__builtin_fmaf(cvt_ubyte<0>(t0), s, ns8), __builtin_fmaf(cvt_ubyte<0>(t1), s, ns8));
+  d[1] = pack_bf16x2_rne(__builtin_fmaf(cvt_ubyte<1>(t0), s, ns8), __builtin_fmaf(cvt_ubyte<1>(t1), s, ns8));
+  d[2] = pack_bf16x2_rne(__builtin_fmaf(cvt_ubyte<2>(t0), s, ns8), __builtin_fmaf(cvt_ubyte<2>(t1), s, ns8));
+  d[3] = pack_bf16x2_rne(__builtin_fmaf(cvt_ubyte<3>(t0), s, ns8), __builtin_fmaf(cvt_ubyte<3>(t1), s, ns8));
   return d;
 }
 
@@ -133,24 +144,52 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  uint32_t vmask;
+  asm volatile("v_mov_b32 %0, 0x0F0F0F0F" : "=v"(vmask));
+
+  // One 64-k block: four k16 steps, software-pipelined: while the 16 MFMAs of step s run, the
+  // A fragments of step s + 1 are read from LDS and its B fragments dequantized; the group
+  // barriers interleave them (1 MFMA, a few VALU ops, an LDS read, ...).
   auto compute = [&](int stage, const WRegs& r) {
     const uint16_t* as = As[stage];
+    float sc[NJ], ns8[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      sc[j] = bf16_bits_to_f32(r.s[j]);
+      ns8[j] = -8.f * sc[j];
+    }
+    u32x4_t af[2][MI], bf[2][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+      af[0][i] = *reinterpret_cast<const u32x4_t*>(&as[(32 * i + ln) * LDA + 32 * kh]);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) bf[0][j] = dequant_word_bf16(r.w[j][0], vmask, sc[j], ns8[j]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      u32x4_t bfrag[NJ];
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s < 3) {
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const float sc = bf16_bits_to_f32(r.s[j]);
-        bfrag[j] = dequant_word_bf16(r.w[j][s], sc, -8.f * sc);
+        for (int i = 0; i < MI; ++i)
+          af[nxt][i] = *reinterpret_cast<const u32x4_t*>(&as[(32 * i + ln) * LDA + 32 * kh + 8 * (s + 1)]);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) bf[nxt][j] = dequant_word_bf16(r.w[j][s + 1], vmask, sc[j], ns8[j]);
       }
 #pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const u32x4_t afrag =
-            *reinterpret_cast<const u32x4_t*>(&as[(32 * i + ln) * LDA + 32 * kh + 8 * s]);
+      for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(afrag), as_bf16x8(bfrag[j]),
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(af[cur][i]), as_bf16x8(bf[cur][j]),
                                                               acc[i][j], 0, 0, 0);
+      if (s < 3) {
+        // MI * NJ MFMAs; NJ * 23 dequant VALU ops and MI LDS reads spread between them.
+        constexpr int kMfma = MI * NJ;
+        constexpr int kValu = (NJ * 23 + kMfma - 1) / kMfma;
+#pragma unroll
+        for (int k = 0; k < kMfma; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);  // VALU
+          if (k < MI) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        }
       }
     }
   };
@@ -198,6 +237,201 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// v2 pipeline (K % 64 == 0, G a power of two >= 32): activations go global -> LDS directly with
+// buffer loads into LDS (no staging registers), through a ring of ST stages; weights go to a
+// ring of ST register slots. At block kb the loads for block kb + ST - 1 are issued, so ST - 1
+// blocks of both are in flight while one is computed. Per block: one explicit wait for this
+// wave's loads of the block, one barrier (all waves' LDS writes visible, and the stage about to
+// be refilled is no longer read), then the loads for block kb + ST - 1, then the MFMAs.
+//
+// LDS activation layout: row-major rows of 64 bf16 (128 B, eight 16-byte chunks) with the chunk
+// index XOR-swizzled by (row >> 1) & 7, so the 16-byte fragment reads of 16 consecutive rows hit
+// 16 distinct bank groups. A 16-byte LDS load by lane L lands at base + 16 L, so each load
+// instruction fills 8 rows: lane L fetches row L / 8, chunk (L % 8) ^ ((row >> 1) & 7).
+// Rows past M and blocks past K read as zero through the buffer range check.
+
+// One 16-byte buffer load per lane into LDS at dst + 16 * lane. (A plain device function: the
+// builtin inside a lambda of a kernel template keeps the host pass from emitting the launch stub.)
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint16_t* dst, uint32_t voff,
+                                           uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff,
+                                           soff, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_c() {
+  // s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0], expcnt, lgkmcnt, vmcnt[5:4])
+  constexpr int imm = (N & 0xF) | (0x7 << 4) | (0xF << 8) | (((N >> 4) & 0x3) << 14);
+  __builtin_amdgcn_s_waitcnt(imm);
+}
+
+template <int BM, int WN, int NWN, int ST>
+__global__ __launch_bounds__(NWN * kWave) void w4_gemm2_kernel(
+    const uint16_t* __restrict__ A, const uint32_t* __restrict__ Wq,
+    const uint16_t* __restrict__ S, uint16_t* __restrict__ C, int M, int N, int K, int lgG) {
+  constexpr int THREADS = NWN * kWave;
+  constexpr int MI = BM / 32, NJ = WN / 32, BN = WN * NWN;
+  constexpr int STAGE = BM * BK;                 // bf16 elements per stage
+  constexpr int IPW = BM / (8 * NWN);            // 16-byte LDS-load instructions per wave per block
+  static_assert(BM % (8 * NWN) == 0, "whole LDS-load instructions per wave");
+  constexpr uint32_t kOOB = 0x7fffffc0u;
+  __shared__ __align__(16) uint16_t As[ST * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int KW = K >> 3, KG = K >> lgG;
+  const int KB = K / BK;
+
+  const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(A), (short)0, (int)((size_t)M * K * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(Wq), (short)0, (int)((size_t)N * KW * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(S), (short)0, (int)((size_t)N * KG * 2), 0x00020000);
+
+  // activation loader: this lane's row / swizzled chunk inside each of the wave's instructions
+  uint32_t a_voff[IPW];
+#pragma unroll
+  for (int t = 0; t < IPW; ++t) {
+    const int row = 8 * (wv * IPW + t) + (lane >> 3);
+    const int ch = (lane & 7) ^ ((row >> 1) & 7);
+    a_voff[t] = ((uint32_t)(m0 + row) * (uint32_t)K + 8u * ch) * 2u;
+  }
+  auto issue_a = [&](int stage, int kb) {
+    const uint32_t so = kb < KB ? 128u * kb : kOOB;
+#pragma unroll
+    for (int t = 0; t < IPW; ++t) lds_load16(ares, &As[stage * STAGE + 512 * (wv * IPW + t)], a_voff[t], so);
+  };
+
+  // weight loader: lane (n = lane % 32, kh = lane / 32), 16 bytes (words 4 kh .. 4 kh + 3 of the
+  // block) per n-frag, plus the group scale of those 32 k.
+  const int ln = lane & 31, kh = lane >> 5;
+  uint32_t w_voff[NJ], s_voff[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const uint32_t n = (uint32_t)(n0 + wv * WN + 32 * j + ln);
+    w_voff[j] = n * (uint32_t)KW * 4u + 16u * kh;
+    s_voff[j] = n * (uint32_t)KG * 2u;
+  }
+  struct WRegs {
+    u32x4_t w[NJ];
+    uint32_t s[NJ];
+  };
+  auto issue_w = [&](WRegs& r, int kb) {
+    const bool live = kb < KB;
+    const uint32_t so = live ? 32u * kb : kOOB;
+    const uint32_t ss = live ? 2u * (uint32_t)((kb * BK + 32 * kh) >> lgG) : kOOB;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      r.w[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wres, w_voff[j], so, 0));
+      r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sres, s_voff[j] + ss, 0, 0);
+    }
+  };
+
+  f32x16_t acc[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  uint32_t vmask;
+  asm volatile("v_mov_b32 %0, 0x0F0F0F0F" : "=v"(vmask));
+  // LDS offset (elements) of this lane's A fragment: row 32 i + ln, chunk 4 kh + s (swizzled)
+  auto a_frag = [&](const uint16_t* as, int i, int s) {
+    const int row = 32 * i + ln;
+    const int ch = (4 * kh + s) ^ ((row >> 1) & 7);
+    return *reinterpret_cast<const u32x4_t*>(&as[row * BK + 8 * ch]);
+  };
+
+  auto compute = [&](int stage, const WRegs& r) {
+    const uint16_t* as = &As[stage * STAGE];
+    float sc[NJ], ns8[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      sc[j] = bf16_bits_to_f32(r.s[j]);
+      ns8[j] = -8.f * sc[j];
+    }
+    u32x4_t af[2][MI], bf[2][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) af[0][i] = a_frag(as, i, 0);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) bf[0][j] = dequant_word_bf16(r.w[j][0], vmask, sc[j], ns8[j]);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s < 3) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i) af[nxt][i] = a_frag(as, i, s + 1);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) bf[nxt][j] = dequant_word_bf16(r.w[j][s + 1], vmask, sc[j], ns8[j]);
+      }
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(af[cur][i]), as_bf16x8(bf[cur][j]),
+                                                              acc[i][j], 0, 0, 0);
+      if (s < 3) {
+        constexpr int kMfma = MI * NJ;
+        constexpr int kValu = (NJ * 23 + kMfma - 1) / kMfma;
+#pragma unroll
+        for (int k = 0; k < kMfma; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);
+          if (k < MI) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      }
+    }
+  };
+
+  // loads of one block per wave: IPW activation loads, NJ weight loads, NJ scale loads
+  constexpr int LPB = IPW + 2 * NJ;
+  WRegs wr[ST];
+#pragma unroll
+  for (int p = 0; p < ST - 1; ++p) {  // each block's loads stay contiguous in issue order
+    __builtin_amdgcn_sched_barrier(0);
+    issue_a(p, p);
+    issue_w(wr[p], p);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int kb0 = 0; kb0 < KB; kb0 += ST) {
+#pragma unroll
+    for (int u = 0; u < ST; ++u) {
+      const int kb = kb0 + u;
+      wait_vmcnt_c<LPB * (ST - 2)>();  // this wave's loads of block kb have landed
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      issue_a((u + ST - 1) % ST, kb + ST - 1);
+      issue_w(wr[(u + ST - 1) % ST], kb + ST - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kb < KB) compute(u, wr[u]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  wait_vmcnt_c<0>();  // the trailing out-of-range loads have landed before the LDS is released
+
+  // ---- epilogue: D[i][j] of lane l, register r: j = l % 32, i = 8 (r / 4) + 4 (l / 32) + r % 4
+  const bool full = m0 + BM <= M && n0 + BN <= N;
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int n = n0 + wv * WN + 32 * j + ln;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
+        if (full || (m < M && n < N)) C[(size_t)m * N + n] = (uint16_t)f32_to_bf16_rne(acc[i][j][r]);
+      }
+    }
+}
+
+inline int ilog2(int g) { return 31 - __builtin_clz((unsigned)g); }
+
 struct TileCfg {
   int bm, bn;
   float eff;  // relative per-tile efficiency used by the planner
@@ -207,17 +441,32 @@ constexpr TileCfg kCfgs[] = {
     {256, 128, 0.90f},  // 1: BM 256, 4 waves x 32 cols
     {128, 256, 0.85f},  // 2: BM 128, 4 waves x 64 cols
     {128, 128, 0.75f},  // 3: BM 128, 4 waves x 32 cols
+    {128, 128, 1.00f},  // 4: v2, BM 128, 4 waves x 32 cols, 3 stages
+    {128, 128, 1.00f},  // 5: v2, BM 128, 4 waves x 32 cols, 4 stages
+    {128, 256, 1.00f},  // 6: v2, BM 128, 4 waves x 64 cols, 3 stages
+    {256, 128, 1.00f},  // 7: v2, BM 256, 4 waves x 32 cols, 3 stages
+    {64, 128, 1.00f},   // 8: v2, BM 64, 4 waves x 32 cols, 4 stages
 };
 
 }  // namespace
+
+// The v2 kernel addresses A, Wq and S through 32-bit buffer offsets (rows up to M + 256 included)
+// and reads whole 64-k blocks whose 32-k halves sit inside one power-of-two group.
+bool gemm_v2_ok(int M, int N, int K, int G) {
+  if (K % 64 != 0 || G < 32 || (G & (G - 1)) != 0) return false;
+  const uint64_t limit = 0x7fffffffull;
+  return (uint64_t)(M + 256) * K * 2 < limit && (uint64_t)N * K / 2 < limit &&
+         (uint64_t)N * (K / G) * 2 < limit;
+}
 
 GemmPlan gemm_plan(int M, int N, int K, int G) {
   (void)K;
   (void)G;
   constexpr int kCUs = 256;
+  if (gemm_v2_ok(M, N, K, G)) return GemmPlan{4, kCfgs[4].bm, kCfgs[4].bn};
   int best = 0;
   double best_cost = 1e300;
-  for (int c = 0; c < (int)(sizeof(kCfgs) / sizeof(kCfgs[0])); ++c) {
+  for (int c = 0; c < 4; ++c) {
     const long tiles = (long)((M + kCfgs[c].bm - 1) / kCfgs[c].bm) * ((N + kCfgs[c].bn - 1) / kCfgs[c].bn);
     const long rounds = (tiles + kCUs - 1) / kCUs;
     const double cost = (double)rounds * kCfgs[c].bm * kCfgs[c].bn / kCfgs[c].eff;
@@ -247,6 +496,26 @@ hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
     case 3:
       hipLaunchKernelGGL((w4_gemm_kernel<128, 32, 4>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
                          a.C, a.M, a.N, a.K, a.G);
+      return hipSuccess;
+    case 4:
+      hipLaunchKernelGGL((w4_gemm2_kernel<128, 32, 4, 3>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
+                         a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 5:
+      hipLaunchKernelGGL((w4_gemm2_kernel<128, 32, 4, 4>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
+                         a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 6:
+      hipLaunchKernelGGL((w4_gemm2_kernel<128, 64, 4, 3>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
+                         a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 7:
+      hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 3>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
+                         a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 8:
+      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
+                         a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     default:
       return hipErrorInvalidValue;
