@@ -37,6 +37,20 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA (256 CU x 4096 flop/clk x 2.4 GHz)
 G = 128
 ROTATE_BYTES = int(1.1 * (1 << 30))
+# HBM bytes per launch of the dominant kernel, from FETCH_SIZE / WRITE_SIZE counter passes scaled
+# by a 1 GiB copy's readings (the summary holds the commands and the arithmetic).
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "w4_gemv_m1_kernel.gate_up_m1.md")
+
+
+def profiled_traffic(path):
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def parse():
@@ -47,6 +61,11 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-extra", action="store_true", help="headline only")
     p.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU baseline time budget")
+    p.add_argument("--dominant-only", action="store_true",
+                   help="only the dominant-kernel launches (gate_up, M=1), e.g. under a profiler")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only 1 GiB device-to-device copies: the known-size reference for HBM "
+                        "byte counters read under a profiler")
     return p.parse_args()
 
 
@@ -63,6 +82,15 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel(), "copy_bytes_written": dst.numel(),
+                          "launches": 8}), flush=True)
+        return
     kern = Kernels()
     dev = torch.device("cuda", 0)
 
@@ -124,15 +152,17 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1)  # ms
 
-    # ---------------- headline: M=1 set, exactly args.steps steps
-    g_warm = graph_of(lambda i: step(x1, i), max(args.warmup, 1))
-    g_main = graph_of(lambda i: step(x1, i), args.steps)
-    if args.warmup > 0:
-        time_graph(g_warm)
-    ms_total = time_graph(g_main)
-    ms_step = ms_total / args.steps
     bytes_m1 = sum(synth.gemv_bytes(1, N, K, G) for _, N, K in layers)
-    value = bytes_m1 / (ms_step * 1e-3) / 1e9
+    value = ms_step = None
+    if not args.dominant_only:
+        # ---------------- headline: M=1 set, exactly args.steps steps
+        g_warm = graph_of(lambda i: step(x1, i), max(args.warmup, 1))
+        g_main = graph_of(lambda i: step(x1, i), args.steps)
+        if args.warmup > 0:
+            time_graph(g_warm)
+        ms_total = time_graph(g_main)
+        ms_step = ms_total / args.steps
+        value = bytes_m1 / (ms_step * 1e-3) / 1e9
 
     # ---------------- dominant kernel: gate+up GEMV, M=1, back-to-back launches
     n_launch = 4 * copies
@@ -143,9 +173,14 @@ def main():
     bytes_gu = synth.gemv_bytes(1, N_gu, K_gu, G)
     achieved = bytes_gu / (ms_gu * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "w4_gemv_mfma_kernel (gate_up 37888x3584, M=1)",
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": profiled_traffic(TRAFFIC_PROFILE),
+                "kernel": "w4_gemv_m1_kernel (gate_up 37888x3584, M=1)",
                 "bytes_per_launch": bytes_gu, "avg_launch_us": round(ms_gu * 1e3, 3)}
+
+    if args.dominant_only:
+        print(json.dumps({"roofline": roofline, "launches": 6 * n_launch}), flush=True)
+        return
 
     extra = {}
     if not args.no_extra:

@@ -212,3 +212,29 @@ def test_repeat_runs_are_bitwise_deterministic(kernels):
     a = to_host_bits(kernels.w4_linear(xd, wd, sd, G))
     b = to_host_bits(kernels.w4_linear(xd, wd, sd, G))
     np.testing.assert_array_equal(a, b)
+
+
+# ----------------------------------------------------------------- committed golden fixtures
+def _golden(name):
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name + ".npz")
+    with np.load(path) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_golden_ref_case_gemv(kernels, M):
+    c = _golden("ref_case")
+    y = run_linear(kernels, c["X"][:M], c["Wq"], c["S"], int(c["G"]))
+    check_bf16_faithful(y, c["y_exact"][:M].astype(np.float64), 1e-5)
+
+
+def test_golden_edge_case(kernels):
+    c = _golden("edge_case")
+    G = int(c["G"])
+    Wq, S = kernels.w4_quantize(to_dev(c["W"], torch.bfloat16), G)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_host_bits(Wq), c["Wq"])
+    np.testing.assert_array_equal(to_host_bits(S), c["S"])
+    y = run_linear(kernels, c["X"], c["Wq"], c["S"], G)
+    check_bf16_faithful(y, c["y_exact"].astype(np.float64), 1e-5)
