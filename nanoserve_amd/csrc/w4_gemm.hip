@@ -437,15 +437,12 @@ struct TileCfg {
   float eff;  // relative per-tile efficiency used by the planner
 };
 constexpr TileCfg kCfgs[] = {
-    {256, 256, 1.00f},  // 0: BM 256, 4 waves x 64 cols
-    {256, 128, 0.90f},  // 1: BM 256, 4 waves x 32 cols
-    {128, 256, 0.85f},  // 2: BM 128, 4 waves x 64 cols
-    {128, 128, 0.75f},  // 3: BM 128, 4 waves x 32 cols
+    {256, 256, 1.00f},  // 0: v1, BM 256, 4 waves x 64 cols
+    {256, 128, 0.90f},  // 1: v1, BM 256, 4 waves x 32 cols
+    {128, 256, 0.85f},  // 2: v1, BM 128, 4 waves x 64 cols
+    {128, 128, 0.75f},  // 3: v1, BM 128, 4 waves x 32 cols
     {128, 128, 1.00f},  // 4: v2, BM 128, 4 waves x 32 cols, 3 stages
-    {128, 128, 1.00f},  // 5: v2, BM 128, 4 waves x 32 cols, 4 stages
-    {128, 256, 1.00f},  // 6: v2, BM 128, 4 waves x 64 cols, 3 stages
-    {256, 128, 1.00f},  // 7: v2, BM 256, 4 waves x 32 cols, 3 stages
-    {64, 128, 1.00f},   // 8: v2, BM 64, 4 waves x 32 cols, 4 stages
+    {64, 128, 1.00f},   // 5: v2, BM 64, 4 waves x 32 cols, 4 stages
 };
 
 }  // namespace
@@ -463,7 +460,12 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
   (void)K;
   (void)G;
   constexpr int kCUs = 256;
-  if (gemm_v2_ok(M, N, K, G)) return GemmPlan{4, kCfgs[4].bm, kCfgs[4].bn};
+  if (gemm_v2_ok(M, N, K, G)) {
+    // 128 x 128 tiles (three workgroups per CU) unless they leave CUs idle; then 64 x 128.
+    const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
+    const int c = tiles < kCUs ? 5 : 4;
+    return GemmPlan{c, kCfgs[c].bm, kCfgs[c].bn};
+  }
   int best = 0;
   double best_cost = 1e300;
   for (int c = 0; c < 4; ++c) {
@@ -502,18 +504,6 @@ hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
                          a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     case 5:
-      hipLaunchKernelGGL((w4_gemm2_kernel<128, 32, 4, 4>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
-                         a.C, a.M, a.N, a.K, ilog2(a.G));
-      return hipSuccess;
-    case 6:
-      hipLaunchKernelGGL((w4_gemm2_kernel<128, 64, 4, 3>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
-                         a.C, a.M, a.N, a.K, ilog2(a.G));
-      return hipSuccess;
-    case 7:
-      hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 3>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
-                         a.C, a.M, a.N, a.K, ilog2(a.G));
-      return hipSuccess;
-    case 8:
       hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
                          a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;

@@ -403,54 +403,57 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
 //    table (double-buffered by group parity); after the group's barrier, 16 lanes per row sum
 //    the row's C partials and wave (i % NW) writes Y.
 //  * Blocks stream through a ring of R register slots (R - 1 blocks in flight per wave),
-//    continuing across row groups.
+//    continuing across row groups; the ring's refill cursor (group, slot) advances
+//    incrementally in scalar registers.
+//  * Branch-free inner loop: the per-chunk offsets are stored four times (one 16-byte LDS read
+//    initialises the whole MFMA accumulator), the diagonal value is picked with three selects,
+//    and lanes off the diagonal (or on a padded slot) write to a private dummy slot.
 template <int NW, int R>
 __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
     const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int N, int K) {
-  constexpr uint32_t kOOB = 0x7fffffc0u;  // buffer offset past any range: reads return zero
+  constexpr uint32_t kOOB = 0x7fffffc0u;
+  constexpr int XR = 136;
   extern __shared__ __align__(16) unsigned char smem[];
   const int C = K >> 7, KV = K >> 3;
-  const int CP = (C + 15) & ~15;                                       // padded for the xs pass
-  // X in LDS, pair order, one 128-element chunk per 136-element row: the 16-byte row padding
-  // puts the 16 lanes that read 16 different chunks on 16 different bank groups.
-  constexpr int XR = 136;
-  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                    // [CP][136]
-  float* xs = reinterpret_cast<float*>(smem + (size_t)CP * XR * 2);    // [CP]
-  float* part = xs + CP;                                               // [2][16 C]
+  const int CP = (C + 15) & ~15;
+  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                      // [CP][136]
+  f32x4_t* xs4 = reinterpret_cast<f32x4_t*>(smem + (size_t)CP * XR * 2); // [CP]
+  float* part = reinterpret_cast<float*>(xs4 + CP);                      // [2][16 C] + 64 dummies
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15, kg = lane >> 4;
   const int ngroups = (N + 15) >> 4;
   const int gstep = gridDim.x;
-  // Every wave runs nbp block slots per group (a multiple of R); wave wv's slot i is block
-  // b = wv + NW i of the group, and slots with b >= C are padding (no memory traffic).
   const int nbp = R * ((C + NW * R - 1) / (NW * R));
 
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(Wq), (short)0, (int)((size_t)N * (K >> 1)), 0x00020000);
   const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(S), (short)0, (int)((size_t)N * C * 2), 0x00020000);
-  const uint32_t vw = 64u * j + 16u * kg;  // this lane's bytes inside a 1 KiB block
-  const uint32_t vs = 2u * j;              // this lane's scale among a block's 16
+  const uint32_t vw = 64u * j + 16u * kg;
+  const uint32_t vs = 2u * j;
 
-  // Block (g, b) covers the group's pieces 16 b .. 16 b + 15, i.e. flat block g C + b.
-  auto issue = [&](u32x4_t& w, uint32_t& sc, int g, int i) {
-    const int b = wv + NW * i;
-    const bool live = g < ngroups && b < C;
-    const uint32_t blk = (uint32_t)(g * C + b);
+  // refill cursor: (group gr, slot ir) in this wave's stream; slot i is block wv + NW i
+  int gr = blockIdx.x, ir = 0;
+  auto issue = [&](u32x4_t& w, uint32_t& sc) {
+    const int b = wv + NW * ir;
+    const bool live = gr < ngroups && b < C;
+    const uint32_t blk = (uint32_t)(gr * C + b);
     w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                         wres, vw, live ? 1024u * blk : kOOB, 0));
     sc = __builtin_amdgcn_raw_buffer_load_b16(sres, vs, live ? 32u * blk : kOOB, 0);
+    if (++ir == nbp) {
+      ir = 0;
+      gr += gstep;
+    }
   };
 
-  int g = blockIdx.x;
-  // The first R slots are in flight while X is staged.
   u32x4_t ring[R];
   uint32_t rsc[R];
 #pragma unroll
-  for (int u = 0; u < R; ++u) issue(ring[u], rsc[u], g, u);
+  for (int u = 0; u < R; ++u) issue(ring[u], rsc[u]);
   __builtin_amdgcn_sched_barrier(0);
 
   const u32x4_t* x4 = reinterpret_cast<const u32x4_t*>(X);
@@ -458,7 +461,6 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     *reinterpret_cast<u32x4_t*>(&xl[(e >> 4) * XR + 8 * (e & 15)]) =
         e < KV ? pair_order(x4[e]) : u32x4_t{0u, 0u, 0u, 0u};
   __syncthreads();
-  // xs[c] = -136 * sum of x over chunk c: MFMA with A = -136, B column j = chunk cg + j.
   const u32x4_t kNeg136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
   for (int cg = 16 * wv; cg < CP; cg += 16 * NW) {
     const uint16_t* xr = &xl[XR * (cg + j) + 32 * kg];
@@ -467,49 +469,51 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     for (int s4 = 0; s4 < 4; ++s4)
       d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
           as_bf16x8(kNeg136), as_bf16x8(*reinterpret_cast<const u32x4_t*>(xr + 8 * s4)), d, 0, 0, 0);
-    if (kg == 0) xs[cg + j] = d[0];
+    if (kg == 0) xs4[cg + j] = f32x4_t{d[0], d[0], d[0], d[0]};
   }
   __syncthreads();
 
   uint32_t vmask;
   asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(vmask));
   const uint32_t sbits = 0x43004300u;
-  const bool diag = kg == (j >> 2);  // this lane holds D[j][j], in register j % 4
+  const bool diag = kg == (j >> 2);
   const int dr = j & 3;
-  // Chunk of piece j of slot i: (16 (wv + NW i) + j) % C, advanced incrementally.
+  const bool s1 = dr == 1, s2 = dr == 2, s3 = dr == 3;
+  float* dummy = part + 2 * 16 * C + lane;
   const int c_first = (16 * wv + j) % C;
   const int c_step = (16 * NW) % C;
+  int g = blockIdx.x;
   for (int it = 0; g < ngroups; ++it, g += gstep) {
-    float* pt = part + (it & 1) * 16 * C;
+    float* pt = part + (it & 1) * 16 * C + j;
     int c = c_first;
     for (int i0 = 0; i0 < nbp; i0 += R) {
 #pragma unroll
       for (int u = 0; u < R; ++u) {
         const int b = wv + NW * (i0 + u);
-        const f32x4_t init = {xs[c], xs[c], xs[c], xs[c]};
+        f32x4_t t = xs4[c];
         const uint16_t* xr = &xl[XR * c + 32 * kg];
-        f32x4_t t = init;
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4)
           t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
               as_bf16x8(*reinterpret_cast<const u32x4_t*>(xr + 8 * s4)),
               as_bf16x8(unpack_word_paired(ring[u][s4], vmask, sbits)), t, 0, 0, 0);
-        const float v = dr == 0 ? t[0] : dr == 1 ? t[1] : dr == 2 ? t[2] : t[3];
-        if (b < C && diag) pt[16 * b + j] = bf16_bits_to_f32(rsc[u] & 0xffffu) * v;
+        float v = s1 ? t[1] : t[0];
+        v = s2 ? t[2] : v;
+        v = s3 ? t[3] : v;
+        float* dst = diag && b < C ? pt + 16 * b : dummy;
+        *dst = bf16_bits_to_f32(rsc[u] & 0xffffu) * v;
         c += c_step;
         c = c >= C ? c - C : c;
         __builtin_amdgcn_sched_barrier(0);
-        // Refill: slot i0 + u + R of this group, or slot i0 + u + R - nbp of the next group.
-        const bool wrap = i0 + R >= nbp;
-        issue(ring[u], rsc[u], wrap ? g + gstep : g, wrap ? u : i0 + R + u);
+        issue(ring[u], rsc[u]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
     __syncthreads();
     if (wv == it % NW) {
-      // Rows of the group: lane (row j, part kg) sums chunks kg, kg + 4, ...; then 4-lane sum.
+      const float* pr = part + (it & 1) * 16 * C;
       float v = 0.f;
-      for (int cc = kg; cc < C; cc += 4) v += pt[j * C + cc];
+      for (int cc = kg; cc < C; cc += 4) v += pr[j * C + cc];
       v += __shfl_xor(v, 16, kWave);
       v += __shfl_xor(v, 32, kWave);
       const int n = 16 * g + j;
@@ -520,8 +524,9 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
 
 size_t m1_bytes(int K) {
   const int C = K >> 7, CP = (C + 15) & ~15;
-  return (size_t)CP * 136 * 2 + (size_t)CP * 4 + (size_t)2 * 16 * C * 4;
+  return (size_t)CP * 136 * 2 + (size_t)CP * 16 + (size_t)(2 * 16 * C + 64) * 4;
 }
+
 
 // Generic fallback: one wavefront per output row, exact fp32 dequant, fp32 FMA.
 template <int MMAX>
@@ -615,35 +620,26 @@ hipError_t launch_m1(const GemvArgs& a, hipStream_t st) {
   int cus = 0;
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
   if (e != hipSuccess) return e;
+  // Two workgroups per CU: more resident waves only lengthen the memory queues.
   const int ngroups = (a.N + 15) / 16;
-  const int grid = max(1, min(ngroups, max(per_cu, 1) * cus));
+  const int grid = max(1, min(ngroups, min(max(per_cu, 1), 2) * cus));
   hipLaunchKernelGGL((w4_gemv_m1_kernel<NW, R>), dim3(grid), dim3(NW * kWave), lds, st, a.X, a.Wq,
                      a.S, a.Y, a.N, a.K);
   return hipSuccess;
 }
 
-// (NW, R) for the M = 1 kernel. With fewer 16-row groups than twice the CU count, 14 or 16
-// waves per group (split K further) so every CU keeps enough loads in flight, with the deeper
-// ring once each wave has >= 8 blocks per group; otherwise 7 or 8 waves with a 4-deep ring,
-// whichever pads fewer block slots.
+// (NW, R) for the M = 1 kernel, from sweeps on MI355X: a 2-slot ring; 16 waves per group
+// when K is long (many blocks per group), 14 when there are many groups (exactly two blocks
+// per wave at K = 3584), otherwise 8.
 void m1_choose(int N, int K, int& nw, int& r) {
   const int C = K >> 7, groups = (N + 15) / 16;
-  auto waste = [&](int n, int rr) {
-    const int nbp = rr * ((C + n * rr - 1) / (n * rr));
-    return n * nbp - C;
-  };
-  if (groups < 512 && C >= 14) {
-    if (C >= 128) {
-      nw = 16;
-      r = 4;
-    } else {
-      r = 2;
-      nw = waste(14, 2) < waste(16, 2) ? 14 : 16;
-    }
-    return;
-  }
-  r = 4;
-  nw = C >= 8 && waste(7, 4) < waste(8, 4) ? 7 : (C >= 8 ? 8 : 3);
+  r = 2;
+  if (C >= 64)
+    nw = 16;
+  else if (groups >= 1024 && C >= 14)
+    nw = 14;
+  else
+    nw = 8;
 }
 
 }  // namespace
@@ -691,12 +687,7 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
   if (p.m1) {
     if (p.nw == 16 && p.rt == 2) return launch_m1<16, 2>(a, st);
     if (p.nw == 14 && p.rt == 2) return launch_m1<14, 2>(a, st);
-    if (p.nw == 16 && p.rt == 4) return launch_m1<16, 4>(a, st);
-    if (p.nw == 8 && p.rt == 4) return launch_m1<8, 4>(a, st);
     if (p.nw == 8 && p.rt == 2) return launch_m1<8, 2>(a, st);
-    if (p.nw == 7 && p.rt == 4) return launch_m1<7, 4>(a, st);
-    if (p.nw == 4 && p.rt == 4) return launch_m1<4, 4>(a, st);
-    if (p.nw == 3 && p.rt == 4) return launch_m1<3, 4>(a, st);
     return hipErrorInvalidValue;
   }
   if (p.xlds) {
