@@ -528,6 +528,189 @@ size_t m1_bytes(int K) {
 }
 
 
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8],
+// vmcnt[5:4] in bits 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  constexpr int imm = (N & 0xF) | (0x7 << 4) | (0x0 << 8) | (((N >> 4) & 0x3) << 14);
+  __builtin_amdgcn_s_waitcnt(imm);
+}
+
+// 16 bytes per lane from a buffer into LDS at dst + 16 * lane (a plain device function: the
+// builtin inside a lambda of a kernel template keeps the host pass from emitting the stub).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff,
+                                           soff, 0, 0);
+}
+
+// LDS-staged GEMV for M = 1..8 and K <= 32 x 128 (whole rows of a 16-row group fit in LDS).
+//  * HBM sees contiguous row segments: each 16-row group (16 rows x K/2 bytes) and its scales
+//    (16 x K/128 bf16, contiguous in S) are copied straight into LDS by buffer-to-LDS loads
+//    (up to 1 KiB of one row per wave instruction), into one of two stages; rows are padded
+//    by 16 bytes so a fragment read of 16 rows hits 16 different bank groups.
+//  * The MFMAs are row-tiled (v_mfma_f32_16x16x32_bf16, A = activations, B = weights of the
+//    16 rows): wave w owns chunks (128 k) w, w + NW, ... of every group and keeps their
+//    activation fragments (pair order) in registers for the whole kernel, together with the
+//    accumulator initialiser -136 * sum_k x[m][k] per chunk, computed once by an MFMA with a
+//    constant -136 operand (it lands directly in the accumulator layout).
+//  * Weights as exact bf16 128 + q (paired-nibble unpack), fp32 scale per (row, chunk) after
+//    each chunk: the same exact dequant as the other GEMV kernels.
+//  * One barrier per group: after it, the next group's loads are issued into the other stage,
+//    the group is computed, and each wave leaves its partial sums in a double-buffered LDS
+//    area; wave (it % NW) reduces them after the following barrier and writes Y.
+template <int MP, int NW, int CW, int ST, int DPW>
+__global__ __launch_bounds__(NW * kWave) void w4_gemv_lds_kernel(
+    const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
+    const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int M, int N, int K) {
+  constexpr uint32_t kOOB = 0x7fffffc0u;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int C = K >> 7;
+  const int RS = 64 * C + 16;                      // LDS row stride (bytes)
+  const int STG = 16 * RS;                         // one stage of weights
+  const int IPR = (C + 15) >> 4;                   // DMA instructions per row
+  unsigned char* wst = smem;                                          // [ST][16][RS]
+  uint16_t* sst = reinterpret_cast<uint16_t*>(smem + ST * STG);           // [ST][16 C]
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(sst + ST * 16 * C);           // [2][NW][64]
+  unsigned char* dummy = reinterpret_cast<unsigned char*>(red + 2 * NW * 64);  // 1 KiB sink
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15, kg = lane >> 4;
+  const int ngroups = (N + 15) >> 4;
+  const int gstep = gridDim.x;
+  const uint32_t RB = (uint32_t)(K >> 1);          // bytes per weight row
+
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(Wq), (short)0, (int)((size_t)N * RB), 0x00020000);
+  const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(S), (short)0, (int)((size_t)N * C * 2), 0x00020000);
+
+  // group g -> stage st: copy q (of 16 IPR + 1) is row q / IPR, bytes [1024 h, ...) with
+  // h = q % IPR, or the group's 32 C scale bytes for q = 16 IPR. Wave w issues copies
+  // w, w + NW, ... and pads to exactly DPW copies (extra ones read out of range into a sink),
+  // so every wave has the same, compile-time number of copies per group in flight.
+  auto issue_group = [&](int g, int st) {
+    const bool live = g < ngroups;
+#pragma unroll
+    for (int t = 0; t < DPW; ++t) {
+      const int q = wv + NW * t;
+      if (q < 16 * IPR) {
+        const int r = q / IPR, h = q - r * IPR;
+        if (1024 * h + 16 * lane < 64 * C)
+          dma16(wres, wst + st * STG + r * RS + 1024 * h,
+                (uint32_t)(16 * g + r) * RB + 1024u * h + 16u * lane, live ? 0u : kOOB);
+      } else if (q == 16 * IPR) {
+        if (16 * lane < 32 * C)
+          dma16(sres, sst + st * 16 * C, 32u * (uint32_t)C * (uint32_t)g + 16u * lane, live ? 0u : kOOB);
+      } else {
+        dma16(wres, dummy, 0u, kOOB);
+      }
+    }
+  };
+
+  int g = blockIdx.x;
+#pragma unroll
+  for (int p = 0; p < ST - 1; ++p) issue_group(g + p * gstep, p);
+
+  // activation fragments of this wave's chunks: lane (i = l % 16, kg), step s: row m = i
+  // (MP = 1: row 0 on every lane), k = 128 c + 32 kg + 8 s .. + 7 (the k of word 4 kg + s of
+  // the weight lane (n, kg)), pair order
+  u32x4_t xa[CW][4];
+  f32x4_t xi[CW];
+  const u32x4_t kNeg136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
+  const int mrow = MP == 1 ? 0 : j;
+#pragma unroll
+  for (int t = 0; t < CW; ++t) {
+    const int c = wv + NW * t;
+    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      if (c < C && mrow < M)
+        v = pair_order(*reinterpret_cast<const u32x4_t*>(&X[(size_t)mrow * K + 128 * c + 32 * kg + 8 * s4]));
+      xa[t][s4] = v;
+      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(v), as_bf16x8(kNeg136), d, 0, 0, 0);
+    }
+    xi[t] = d;  // D[m][n] = -136 * sum_k x[m][k]: lane (n, kg) register r holds m = 4 kg + r
+  }
+
+  uint32_t vmask;
+  asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(vmask));
+  const uint32_t sbits = 0x43004300u;
+  const uint32_t voffw = (uint32_t)(j * RS + 16 * kg);  // this lane's bytes of a row chunk
+  int it = 0, st = 0;
+  for (; g < ngroups; ++it, g += gstep, st = st == ST - 1 ? 0 : st + 1) {
+    // this wave's copies of group g have landed (those of the ST - 2 later groups may still be
+    // in flight; a wave's stores in between only make the wait longer), then everyone's
+    wait_vmcnt_lgkm0<DPW * (ST - 2)>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (it > 0 && wv == (it - 1) % NW) {
+      // reduce group g - gstep: output (m, n) = lane 16 (m / 4) + n, register m % 4
+      const f32x4_t* rb = red + ((it - 1) & 1) * NW * 64;
+      f32x4_t v = rb[lane];
+      for (int w = 1; w < NW; ++w) {
+        const f32x4_t u = rb[w * 64 + lane];
+        v[0] += u[0]; v[1] += u[1]; v[2] += u[2]; v[3] += u[3];
+      }
+      const int n = 16 * (g - gstep) + j;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 4 * kg + r;
+        if (m < M && n < N && (MP > 1 || (kg == 0 && r == 0))) Y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v[r]);
+      }
+    }
+    issue_group(g + (ST - 1) * gstep, st == 0 ? ST - 1 : st - 1);
+    const unsigned char* ws = wst + st * STG;
+    const uint16_t* ss = sst + st * 16 * C;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < CW; ++t) {
+      const int c = wv + NW * t;
+      if (c < C) {
+        const u32x4_t wv4 = *reinterpret_cast<const u32x4_t*>(ws + voffw + 64 * c);
+        f32x4_t d = xi[t];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              as_bf16x8(xa[t][s4]), as_bf16x8(unpack_word_paired(wv4[s4], vmask, sbits)), d, 0, 0, 0);
+        const float sc = bf16_bits_to_f32(ss[j * C + c]);
+        acc[0] += sc * d[0];
+        if (MP > 1) {
+          acc[1] += sc * d[1];
+          acc[2] += sc * d[2];
+          acc[3] += sc * d[3];
+        }
+      }
+    }
+    red[(it & 1) * NW * 64 + wv * 64 + lane] = acc;
+  }
+  // last group's reduction
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  if (it > 0 && wv == (it - 1) % NW) {
+    const f32x4_t* rb = red + ((it - 1) & 1) * NW * 64;
+    f32x4_t v = rb[lane];
+    for (int w = 1; w < NW; ++w) {
+      const f32x4_t u = rb[w * 64 + lane];
+      v[0] += u[0]; v[1] += u[1]; v[2] += u[2]; v[3] += u[3];
+    }
+    const int n = 16 * (g - gstep) + j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * kg + r;
+      if (m < M && n < N && (MP > 1 || (kg == 0 && r == 0))) Y[(size_t)m * N + n] = (uint16_t)f32_to_bf16_rne(v[r]);
+    }
+  }
+}
+
+size_t lds_bytes(int K, int nw, int st) {
+  const int C = K >> 7;
+  return (size_t)st * 16 * (64 * C + 16) + (size_t)st * 16 * C * 2 + (size_t)2 * nw * 64 * 16 + 1024;
+}
+
 // Generic fallback: one wavefront per output row, exact fp32 dequant, fp32 FMA.
 template <int MMAX>
 __global__ __launch_bounds__(256) void w4_gemv_generic_kernel(
@@ -628,6 +811,23 @@ hipError_t launch_m1(const GemvArgs& a, hipStream_t st) {
   return hipSuccess;
 }
 
+template <int MP, int NW, int CW, int ST, int DPW>
+hipError_t launch_lds(const GemvArgs& a, hipStream_t st, int grid_cap) {
+  const void* fn = reinterpret_cast<const void*>(&w4_gemv_lds_kernel<MP, NW, CW, ST, DPW>);
+  static const hipError_t attr =
+      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (attr != hipSuccess) return attr;
+  const size_t lds = lds_bytes(a.K, NW, ST);
+  int cus = 0;
+  hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+  if (e != hipSuccess) return e;
+  const int ngroups = (a.N + 15) / 16;
+  const int grid = max(1, min(ngroups, grid_cap * cus));
+  hipLaunchKernelGGL((w4_gemv_lds_kernel<MP, NW, CW, ST, DPW>), dim3(grid), dim3(NW * kWave), lds, st, a.X,
+                     a.Wq, a.S, a.Y, a.M, a.N, a.K);
+  return hipSuccess;
+}
+
 // (NW, R) for the M = 1 kernel, from sweeps on MI355X: a 2-slot ring; 16 waves per group
 // when K is long (many blocks per group), 14 when there are many groups (exactly two blocks
 // per wave at K = 3584), otherwise 8.
@@ -662,6 +862,13 @@ GemvPlan gemv_plan(int M, int N, int K, int G) {
     m1_choose(N, K, p.nw, p.rt);
     return p;
   }
+  // M = 2..8 with whole rows of a 16-row group in LDS (K <= 4096): weights staged in LDS.
+  p.lds = M >= 2 && G == 128 && C <= 32 && small_buf;
+  if (p.lds) {
+    p.nw = C <= 16 ? 8 : 14;
+    p.rt = C <= 28 ? 2 : 3;  // chunks per wave (covers C with nw waves)
+    return p;
+  }
   p.rt = 1;
   p.nw = N >= 16384 ? 4 : 8;
   while (p.nw > 1 && C / p.nw < 2) p.nw /= 2;
@@ -688,6 +895,13 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
     if (p.nw == 16 && p.rt == 2) return launch_m1<16, 2>(a, st);
     if (p.nw == 14 && p.rt == 2) return launch_m1<14, 2>(a, st);
     if (p.nw == 8 && p.rt == 2) return launch_m1<8, 2>(a, st);
+    return hipErrorInvalidValue;
+  }
+  if (p.lds) {
+    // copies per wave per group: 16 rows x ceil(C / 16) row pieces + the scale slab
+    if (p.nw == 8 && p.rt == 2) return launch_lds<8, 8, 2, 3, 3>(a, st, 1);
+    if (p.nw == 14 && p.rt == 2) return launch_lds<8, 14, 2, 3, 3>(a, st, 1);
+    if (p.nw == 14 && p.rt == 3) return launch_lds<8, 14, 3, 3, 3>(a, st, 1);
     return hipErrorInvalidValue;
   }
   if (p.xlds) {
