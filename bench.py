@@ -63,6 +63,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=20.0, help="CPU baseline time budget")
     p.add_argument("--dominant-only", action="store_true",
                    help="only the dominant-kernel launches (gate_up, M=1), e.g. under a profiler")
+    p.add_argument("--gemm-only", action="store_true",
+                   help="only the prefill GEMM launches (config 4), e.g. under a profiler")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only 1 GiB device-to-device copies: the known-size reference for HBM "
                         "byte counters read under a profiler")
@@ -152,6 +154,29 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1)  # ms
 
+    def gemm_set():
+        """config 4: prefill GEMMs, gate_up and down at M = 512 and 2048"""
+        gemm = {}
+        for name, N, K in layers:
+            if name not in ("gate_up", "down"):
+                continue
+            for M in (512, 2048):
+                xa = dev_bits(synth.activations(M, K, seed=M), torch.bfloat16)
+                ws = dev_w[name]
+                reps = 6
+                g = graph_of(lambda i: kern.w4_linear(xa, *ws[i % copies], G), reps)
+                time_graph(g)
+                ms = statistics.median(time_graph(g) for _ in range(3)) / reps
+                tf = synth.gemm_flops(M, N, K) / (ms * 1e-3) / 1e12
+                gemm[f"{name}_m{M}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
+                                        "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+                del xa
+        return gemm
+
+    if args.gemm_only:
+        print(json.dumps({"config4_gemm": gemm_set()}), flush=True)
+        return
+
     bytes_m1 = sum(synth.gemv_bytes(1, N, K, G) for _, N, K in layers)
     value = ms_step = None
     if not args.dominant_only:
@@ -230,23 +255,8 @@ def main():
         extra["config1_gate_m1"] = {"us": round(ms1 * 1e3, 3), "gbs": round(b1 / (ms1 * 1e-3) / 1e9, 1)}
         del c1w, wq0, s0
 
-        # config 4: prefill GEMMs
-        gemm = {}
-        for name, N, K in layers:
-            if name not in ("gate_up", "down"):
-                continue
-            for M in (512, 2048):
-                xa = dev_bits(synth.activations(M, K, seed=M), torch.bfloat16)
-                ws = dev_w[name]
-                reps = 6
-                g = graph_of(lambda i: kern.w4_linear(xa, *ws[i % copies], G), reps)
-                time_graph(g)
-                ms = statistics.median(time_graph(g) for _ in range(3)) / reps
-                tf = synth.gemm_flops(M, N, K) / (ms * 1e-3) / 1e12
-                gemm[f"{name}_m{M}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
-                                        "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
-                del xa
-        extra["config4_gemm"] = gemm
+        extra["config4_gemm"] = gemm_set()
+
 
     # ---------------- CPU baseline (PyTorch CPU dequant + fp32 matmul), full M=1 set
     cpu = None

@@ -253,13 +253,14 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm_kernel(
 
 // Epilogue through LDS (the activation ring is free once the K loop is done). Each wave owns
 // a BMW x WN sub-tile (rows m0 .., columns n0w ..): its 32x32 accumulators are rounded to
-// bf16 and written to a wave-private LDS tile with 2-byte stores (row stride WN + 8 keeps
-// the two row halves of a store on different banks), then read back 16 bytes per lane and
-// stored to Y as whole 16-byte row segments. Rows past M / columns past N are not stored.
-template <int MI, int NJ>
+// bf16 and written to a wave-private LDS tile of row stride LS elements with 2-byte stores
+// (LS = WN + 8, where it fits, keeps the two row halves of a store on different banks), then
+// read back 16 bytes per lane and stored to Y as whole 16-byte row segments. Rows past M /
+// columns past N are not stored.
+template <int MI, int NJ, int LS>
 __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[MI][NJ], uint16_t* lds, uint16_t* C,
                                                int M, int N, int m0, int n0w) {
-  constexpr int WN = 32 * NJ, BMW = 32 * MI, LS = WN + 8;
+  constexpr int WN = 32 * NJ, BMW = 32 * MI;
   const int lane = threadIdx.x & 63, ln = lane & 31, kh = lane >> 5;
 #pragma unroll
   for (int i = 0; i < MI; ++i)
@@ -287,6 +288,26 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[MI][NJ], ui
         if (n + e < N) C[(size_t)m * N + n + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
     }
   }
+}
+
+// Direct epilogue (used when the tile does not fit the LDS ring): one bf16 store per value.
+// D[i][j] of lane l, register r: j = l % 32, i = 8 (r / 4) + 4 (l / 32) + r % 4.
+template <int MI, int NJ>
+__device__ __forceinline__ void store_tile_direct(const f32x16_t (&acc)[MI][NJ], uint16_t* C, int M,
+                                                  int N, int m0, int n0w) {
+  const int lane = threadIdx.x & 63, ln = lane & 31, kh = lane >> 5;
+  const bool full = m0 + 32 * MI <= M && n0w + 32 * NJ <= N;
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int n = n0w + 32 * j + ln;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
+        if (full || (m < M && n < N)) C[(size_t)m * N + n] = (uint16_t)f32_to_bf16_rne(acc[i][j][r]);
+      }
+    }
 }
 
 // One 16-byte buffer load per lane into LDS at dst + 16 * lane. (A plain device function: the
@@ -324,7 +345,8 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm2_kernel(
   static_assert(BM % (8 * NWN) == 0, "whole LDS-load instructions per wave");
   constexpr uint32_t kOOB = 0x7fffffc0u;
   __shared__ __align__(16) uint16_t As[ST * STAGE];
-  static_assert(NWN * BM * (WN + 8) <= ST * STAGE, "epilogue tiles fit in the ring");
+  constexpr int ELS = NWN * BM * (WN + 8) <= ST * STAGE ? WN + 8 : WN;  // epilogue row stride
+  constexpr bool kLdsEpilogue = NWN * BM * ELS <= ST * STAGE;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -464,164 +486,10 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm2_kernel(
 
   wait_vmcnt_c<0>();  // the trailing out-of-range loads have landed before the LDS is reused
   lds_barrier();      // every wave is done reading the ring
-  store_tile_lds<MI, NJ>(acc, &As[wv * BM * (WN + 8)], C, M, N, m0, n0 + wv * WN);
-}
-
-// ---------------------------------------------------------------------------------------------
-// v3 pipeline (same operands, LDS layout and arithmetic as v2; ST >= 4 stages). Per block the
-// barrier sits between k16 steps 2 and 3: by then every wave has waited for its loads of the
-// NEXT block, so step 3 already reads the next block's first fragments and the fragment stream
-// never stalls at a block boundary. The loads issued after that barrier (block kb + ST - 1) go
-// into the stage of block kb - 1, which every wave has finished. Each step issues all of the
-// next step's fragment reads first, then interleaves its MFMAs with the next step's dequant.
-template <int BM, int WN, int ST>
-__global__ __launch_bounds__(4 * kWave) void w4_gemm3_kernel(
-    const uint16_t* __restrict__ A, const uint32_t* __restrict__ Wq,
-    const uint16_t* __restrict__ S, uint16_t* __restrict__ C, int M, int N, int K, int lgG) {
-  constexpr int NWN = 4;
-  constexpr int MI = BM / 32, NJ = WN / 32, BN = WN * NWN;
-  constexpr int STAGE = BM * BK;
-  constexpr int IPW = BM / (8 * NWN);
-  static_assert(ST >= 4, "the mid-block barrier needs two blocks in flight beyond the next");
-  static_assert(BM % (8 * NWN) == 0, "whole LDS-load instructions per wave");
-  constexpr uint32_t kOOB = 0x7fffffc0u;
-  __shared__ __align__(16) uint16_t As[ST * STAGE];
-  static_assert(NWN * BM * (WN + 8) <= ST * STAGE, "epilogue tiles fit in the ring");
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int KW = K >> 3, KG = K >> lgG;
-  const int KB = K / BK;
-
-  const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(A), (short)0, (int)((size_t)M * K * 2), 0x00020000);
-  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint32_t*>(Wq), (short)0, (int)((size_t)N * KW * 4), 0x00020000);
-  const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(S), (short)0, (int)((size_t)N * KG * 2), 0x00020000);
-
-  uint32_t a_voff[IPW];
-#pragma unroll
-  for (int t = 0; t < IPW; ++t) {
-    const int row = 8 * (wv * IPW + t) + (lane >> 3);
-    const int ch = (lane & 7) ^ ((row >> 1) & 7);
-    a_voff[t] = ((uint32_t)(m0 + row) * (uint32_t)K + 8u * ch) * 2u;
-  }
-  auto issue_a = [&](int stage, int kb) {
-    const uint32_t so = kb < KB ? 128u * kb : kOOB;
-#pragma unroll
-    for (int t = 0; t < IPW; ++t) lds_load16(ares, &As[stage * STAGE + 512 * (wv * IPW + t)], a_voff[t], so);
-  };
-  const int ln = lane & 31, kh = lane >> 5;
-  uint32_t w_voff[NJ], s_voff[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    const uint32_t n = (uint32_t)(n0 + wv * WN + 32 * j + ln);
-    w_voff[j] = n * (uint32_t)KW * 4u + 16u * kh;
-    s_voff[j] = n * (uint32_t)KG * 2u;
-  }
-  struct WRegs {
-    u32x4_t w[NJ];
-    uint32_t s[NJ];
-  };
-  auto issue_w = [&](WRegs& r, int kb) {
-    const bool live = kb < KB;
-    const uint32_t so = live ? 32u * kb : kOOB;
-    const uint32_t ss = live ? 2u * (uint32_t)((kb * BK + 32 * kh) >> lgG) : kOOB;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      r.w[j] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wres, w_voff[j], so, 0));
-      r.s[j] = __builtin_amdgcn_raw_buffer_load_b16(sres, s_voff[j] + ss, 0, 0);
-    }
-  };
-
-  f32x16_t acc[MI][NJ];
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int j = 0; j < NJ; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  uint32_t vmask;
-  asm volatile("v_mov_b32 %0, 0x0F0F0F0F" : "=v"(vmask));
-  auto a_frag = [&](int stage, int i, int s) {
-    const int row = 32 * i + ln;
-    const int ch = (4 * kh + s) ^ ((row >> 1) & 7);
-    return *reinterpret_cast<const u32x4_t*>(&As[stage * STAGE + row * BK + 8 * ch]);
-  };
-  auto deq = [&](u32x4_t (&bf)[NJ], const WRegs& r, int s) {
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      const float sc = bf16_bits_to_f32(r.s[j]);
-      bf[j] = dequant_word_bf16(r.w[j][s], vmask, sc, -8.f * sc);
-    }
-  };
-  constexpr int kMfma = MI * NJ;
-  constexpr int kValu = (NJ * 26 + kMfma - 1) / kMfma;
-  // one k16 step: reads of the next operands first, then MFMAs interleaved with the dequant
-  auto step = [&](u32x4_t (&ac)[MI], u32x4_t (&bc)[NJ], u32x4_t (&an)[MI], u32x4_t (&bn)[NJ],
-                  int rstage, int rs, const WRegs& rw, int ds, bool live) {
-#pragma unroll
-    for (int i = 0; i < MI; ++i) an[i] = a_frag(rstage, i, rs);
-    deq(bn, rw, ds);
-    if (live) {
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ac[i]), as_bf16x8(bc[j]),
-                                                              acc[i][j], 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x100, MI, 0);
-#pragma unroll
-    for (int k = 0; k < kMfma; ++k) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);
-    }
-  };
-
-  // Explicit waits count only the LDS-DMA activation loads (see w4_gemm2_kernel).
-  WRegs wr[ST];
-#pragma unroll
-  for (int p = 0; p < ST - 1; ++p) {
-    __builtin_amdgcn_sched_barrier(0);
-    issue_w(wr[p], p);
-    issue_a(p, p);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  wait_vmcnt_c<IPW * (ST - 2)>();  // block 0's activations have landed
-  lds_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-  u32x4_t a0[MI], a1[MI], b0[NJ], b1[NJ];
-#pragma unroll
-  for (int i = 0; i < MI; ++i) a0[i] = a_frag(0, i, 0);
-  deq(b0, wr[0], 0);
-
-  for (int kb0 = 0; kb0 < KB; kb0 += ST) {
-#pragma unroll
-    for (int u = 0; u < ST; ++u) {
-      const int kb = kb0 + u;
-      const bool live = kb < KB;
-      const int nx = (u + 1) % ST;
-      step(a0, b0, a1, b1, u, 1, wr[u], 1, live);
-      step(a1, b1, a0, b0, u, 2, wr[u], 2, live);
-      step(a0, b0, a1, b1, u, 3, wr[u], 3, live);
-      __builtin_amdgcn_sched_barrier(0);
-      wait_vmcnt_c<IPW * (ST - 3)>();  // this wave's activations of block kb + 1 have landed
-      lds_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-      issue_w(wr[(u + ST - 1) % ST], kb + ST - 1);
-      issue_a((u + ST - 1) % ST, kb + ST - 1);
-      __builtin_amdgcn_sched_barrier(0);
-      step(a1, b1, a0, b0, nx, 0, wr[nx], 0, live);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  }
-  wait_vmcnt_c<0>();
-  lds_barrier();
-  store_tile_lds<MI, NJ>(acc, &As[wv * BM * (WN + 8)], C, M, N, m0, n0 + wv * WN);
+  if constexpr (kLdsEpilogue)
+    store_tile_lds<MI, NJ, ELS>(acc, &As[wv * BM * ELS], C, M, N, m0, n0 + wv * WN);
+  else
+    store_tile_direct<MI, NJ>(acc, C, M, N, m0, n0 + wv * WN);
 }
 
 inline int ilog2(int g) { return 31 - __builtin_clz((unsigned)g); }
