@@ -915,7 +915,7 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
     return hipErrorInvalidValue;
   }
 #define NS_GEMV_CASE(RT_, NW_)                                   \
-  if (p.rt == RT_ && p.nw == NW_) return launch_mfma<RT_, NW_, 4>(a, st);
+  if (p.rt == RT_ && p.nw == NW_) return launch_mfma<RT_, NW_, 2>(a, st);
   NS_GEMV_CASE(1, 1)
   NS_GEMV_CASE(1, 2)
   NS_GEMV_CASE(1, 4)
