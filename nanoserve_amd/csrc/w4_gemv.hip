@@ -398,7 +398,8 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
 //    LDS), so D[j][j] = sum x * (q - 8) exactly as in the reference dequant.
 //  * The piece's scale is S[flat piece index] (S is [N][K / 128], i.e. one bf16 per piece in
 //    the same order): 16 consecutive bf16 per block, one 2-byte buffer load per lane.
-//  * Workgroups are persistent over 16-row groups; the C = K / 128 blocks of a group are dealt
+//  * Workgroups are persistent over GR-row groups (GR = 16, or 8: GR C pieces must fill whole
+//    blocks); the GR C / 16 blocks of a group are dealt
 //    to the NW waves round-robin. Each diagonal lane writes scale * D[j][j] to an LDS partial
 //    table (double-buffered by group parity); after the group's barrier, 16 lanes per row sum
 //    the row's C partials and wave (i % NW) writes Y.
@@ -408,7 +409,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
 //  * Branch-free inner loop: the per-chunk offsets are stored four times (one 16-byte LDS read
 //    initialises the whole MFMA accumulator), the diagonal value is picked with three selects,
 //    and lanes off the diagonal (or on a padded slot) write to a private dummy slot.
-template <int NW, int R>
+template <int NW, int R, int GR>
 __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
     const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int N, int K) {
@@ -419,14 +420,15 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   const int CP = (C + 15) & ~15;
   uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                      // [CP][136]
   f32x4_t* xs4 = reinterpret_cast<f32x4_t*>(smem + (size_t)CP * XR * 2); // [CP]
-  float* part = reinterpret_cast<float*>(xs4 + CP);                      // [2][16 C] + 64 dummies
+  float* part = reinterpret_cast<float*>(xs4 + CP);                      // [2][GR C] + 64 dummies
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15, kg = lane >> 4;
-  const int ngroups = (N + 15) >> 4;
+  const int ngroups = (N + GR - 1) / GR;
   const int gstep = gridDim.x;
-  const int nbp = R * ((C + NW * R - 1) / (NW * R));
+  const int NBG = GR * C / 16;  // 1 KiB blocks per group
+  const int nbp = R * ((NBG + NW * R - 1) / (NW * R));
 
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(Wq), (short)0, (int)((size_t)N * (K >> 1)), 0x00020000);
@@ -439,8 +441,8 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   int gr = blockIdx.x, ir = 0;
   auto issue = [&](u32x4_t& w, uint32_t& sc) {
     const int b = wv + NW * ir;
-    const bool live = gr < ngroups && b < C;
-    const uint32_t blk = (uint32_t)(gr * C + b);
+    const bool live = gr < ngroups && b < NBG;
+    const uint32_t blk = (uint32_t)(gr * NBG + b);
     w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                         wres, vw, live ? 1024u * blk : kOOB, 0));
     sc = __builtin_amdgcn_raw_buffer_load_b16(sres, vs, live ? 32u * blk : kOOB, 0);
@@ -479,12 +481,12 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   const bool diag = kg == (j >> 2);
   const int dr = j & 3;
   const bool s1 = dr == 1, s2 = dr == 2, s3 = dr == 3;
-  float* dummy = part + 2 * 16 * C + lane;
+  float* dummy = part + 2 * GR * C + lane;
   const int c_first = (16 * wv + j) % C;
   const int c_step = (16 * NW) % C;
   int g = blockIdx.x;
   for (int it = 0; g < ngroups; ++it, g += gstep) {
-    float* pt = part + (it & 1) * 16 * C + j;
+    float* pt = part + (it & 1) * GR * C + j;
     int c = c_first;
     for (int i0 = 0; i0 < nbp; i0 += R) {
 #pragma unroll
@@ -500,7 +502,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
         float v = s1 ? t[1] : t[0];
         v = s2 ? t[2] : v;
         v = s3 ? t[3] : v;
-        float* dst = diag && b < C ? pt + 16 * b : dummy;
+        float* dst = diag && b < NBG ? pt + 16 * b : dummy;
         *dst = bf16_bits_to_f32(rsc[u] & 0xffffu) * v;
         c += c_step;
         c = c >= C ? c - C : c;
@@ -511,20 +513,21 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     }
     __syncthreads();
     if (wv == it % NW) {
-      const float* pr = part + (it & 1) * 16 * C;
+      const float* pr = part + (it & 1) * GR * C;
       float v = 0.f;
-      for (int cc = kg; cc < C; cc += 4) v += pr[j * C + cc];
+      if (j < GR)
+        for (int cc = kg; cc < C; cc += 4) v += pr[j * C + cc];
       v += __shfl_xor(v, 16, kWave);
       v += __shfl_xor(v, 32, kWave);
-      const int n = 16 * g + j;
-      if (kg == 0 && n < N) Y[n] = (uint16_t)f32_to_bf16_rne(v);
+      const int n = GR * g + j;
+      if (kg == 0 && j < GR && n < N) Y[n] = (uint16_t)f32_to_bf16_rne(v);
     }
   }
 }
 
-size_t m1_bytes(int K) {
+size_t m1_bytes(int K, int gr) {
   const int C = K >> 7, CP = (C + 15) & ~15;
-  return (size_t)CP * 136 * 2 + (size_t)CP * 16 + (size_t)(2 * 16 * C + 64) * 4;
+  return (size_t)CP * 136 * 2 + (size_t)CP * 16 + (size_t)(2 * gr * C + 64) * 4;
 }
 
 
@@ -790,13 +793,13 @@ hipError_t launch_xlds(const GemvArgs& a, hipStream_t st) {
   return hipSuccess;
 }
 
-template <int NW, int R>
+template <int NW, int R, int GR>
 hipError_t launch_m1(const GemvArgs& a, hipStream_t st) {
-  const void* fn = reinterpret_cast<const void*>(&w4_gemv_m1_kernel<NW, R>);
+  const void* fn = reinterpret_cast<const void*>(&w4_gemv_m1_kernel<NW, R, GR>);
   static const hipError_t attr =
       hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
   if (attr != hipSuccess) return attr;
-  const size_t lds = m1_bytes(a.K);
+  const size_t lds = m1_bytes(a.K, GR);
   int per_cu = 0;
   hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NW * kWave, lds);
   if (e != hipSuccess) return e;
@@ -804,9 +807,9 @@ hipError_t launch_m1(const GemvArgs& a, hipStream_t st) {
   e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
   if (e != hipSuccess) return e;
   // Two workgroups per CU: more resident waves only lengthen the memory queues.
-  const int ngroups = (a.N + 15) / 16;
+  const int ngroups = (a.N + GR - 1) / GR;
   const int grid = max(1, min(ngroups, min(max(per_cu, 1), 2) * cus));
-  hipLaunchKernelGGL((w4_gemv_m1_kernel<NW, R>), dim3(grid), dim3(NW * kWave), lds, st, a.X, a.Wq,
+  hipLaunchKernelGGL((w4_gemv_m1_kernel<NW, R, GR>), dim3(grid), dim3(NW * kWave), lds, st, a.X, a.Wq,
                      a.S, a.Y, a.N, a.K);
   return hipSuccess;
 }
@@ -857,9 +860,12 @@ GemvPlan gemv_plan(int M, int N, int K, int G) {
   const int C = K / 128;
   // LDS-activation kernel when X fits and the weight bytes fit a 31-bit buffer offset.
   const bool small_buf = (size_t)N * (K / 2) + (size_t)16 * K < ((size_t)1 << 31);
-  p.m1 = M == 1 && G == 128 && small_buf && m1_bytes(K) <= 96 * 1024;
+  p.m1 = M == 1 && G == 128 && small_buf && m1_bytes(K, 16) <= 96 * 1024;
   if (p.m1) {
     m1_choose(N, K, p.nw, p.rt);
+    // 8-row groups when 16-row groups would give each CU only one or two (measured on qkv)
+    const int groups16 = (N + 15) / 16;
+    p.gr = p.nw == 8 && groups16 > 256 && groups16 < 512 && (K / 128) % 2 == 0 ? 8 : 16;
     return p;
   }
   // M = 2..8 with whole rows of a 16-row group in LDS (K <= 4096): weights staged in LDS.
@@ -892,9 +898,10 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
     return hipSuccess;
   }
   if (p.m1) {
-    if (p.nw == 16 && p.rt == 2) return launch_m1<16, 2>(a, st);
-    if (p.nw == 14 && p.rt == 2) return launch_m1<14, 2>(a, st);
-    if (p.nw == 8 && p.rt == 2) return launch_m1<8, 2>(a, st);
+    if (p.nw == 16 && p.rt == 2 && p.gr == 16) return launch_m1<16, 2, 16>(a, st);
+    if (p.nw == 14 && p.rt == 2 && p.gr == 16) return launch_m1<14, 2, 16>(a, st);
+    if (p.nw == 8 && p.rt == 2 && p.gr == 16) return launch_m1<8, 2, 16>(a, st);
+    if (p.nw == 8 && p.rt == 2 && p.gr == 8) return launch_m1<8, 2, 8>(a, st);
     return hipErrorInvalidValue;
   }
   if (p.lds) {

@@ -21,6 +21,7 @@ struct GemvPlan {
   int rt;     // 16-row tiles per wavefront
   int nw;     // wavefronts per workgroup splitting K
   int sl;     // scale slab loads per lane per tile (LDS-activation kernel)
+  int gr;     // rows per group of the M = 1 kernel (8 or 16)
 };
 
 bool gemv_fast_path_ok(int M, int N, int K, int G);
