@@ -10,8 +10,9 @@ of the step / step time, in GB/s. Inputs are resident in HBM; weight copies rota
 Timing: warmup steps, then exactly --steps steps, each group captured in a HIP graph (no host
 launch gaps inside the timed region), bracketed by synchronize() and HIP events recorded on
 the stream the kernels run on. Also reported under "extra": per-layer launch durations,
-the M=8 set (config 3), the 1.5B gate (config 1), the prefill GEMMs (config 4) and the same
-M=1 step launched eagerly from Python.
+the M=8 set (config 3), the 1.5B gate (config 1), the prefill GEMMs (config 4), the same
+M=1 step launched eagerly from Python, and a whole 28-layer W4 Qwen2.5-7B decode step at
+context 1024 (config 5, tokens/s against its 4.513 GB/token HBM floor).
 
 roofline: the dominant kernel (gate+up GEMV, M=1): algorithmic bytes per launch / its average
 launch duration (HIP events around a graph of back-to-back launches on rotating copies),
@@ -65,6 +66,8 @@ def parse():
                    help="only the dominant-kernel launches (gate_up, M=1), e.g. under a profiler")
     p.add_argument("--gemm-only", action="store_true",
                    help="only the prefill GEMM launches (config 4), e.g. under a profiler")
+    p.add_argument("--decode-only", action="store_true",
+                   help="only the config-5 decode step (28-layer W4 Qwen2.5-7B, context 1024)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only 1 GiB device-to-device copies: the known-size reference for HBM "
                         "byte counters read under a profiler")
@@ -173,8 +176,59 @@ def main():
                 del xa
         return gemm
 
+    def decode_step(reps=40, ctx=1024):
+        """config 5: one decode step of a random-init W4A16 Qwen2.5-7B (28 layers, fused QKV and
+        gate+up, bf16 lm_head) at context 1024 with a bf16 KV cache filled with N(0,1); the step
+        is one HIP graph replay (ns_w4_linear x4, ns_decode_qkv, ns_decode_attention,
+        ns_rmsnorm x2, ns_swiglu per layer; embedding gather and lm_head GEMM in torch)."""
+        from nanoserve_amd.qwen import Qwen2Runner, Qwen2Shape
+
+        shape = Qwen2Shape()
+        runner = Qwen2Runner.random(shape, device=dev, seed=7, kernels=kern)
+        runner.alloc_cache(ctx)
+        gen = torch.Generator(device=dev).manual_seed(8)
+        runner.cache_k.copy_(torch.randn(runner.cache_k.shape, generator=gen, device=dev))
+        runner.cache_v.copy_(torch.randn(runner.cache_v.shape, generator=gen, device=dev))
+        runner.capture_decode()
+        runner.decode(1234, ctx - 1)
+        torch.cuda.synchronize()
+        st = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        times = []
+        for _ in range(5):
+            e0.record(st)
+            for _ in range(reps):
+                runner.graph.replay()
+            e1.record(st)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / reps)
+        ms = statistics.median(times)
+        runner.graph = None
+        for _ in range(3):
+            runner.decode(1234, ctx - 1)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(10):
+            runner.decode(1234, ctx - 1)
+        torch.cuda.synchronize()
+        ms_eager = (time.perf_counter() - t0) * 1e3 / 10
+        finite = bool(torch.isfinite(runner.logits).all())
+        nbytes = shape.decode_bytes(ctx)
+        del runner
+        torch.cuda.empty_cache()
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
+                "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                "bytes_per_token": nbytes, "hbm_floor_ms": round(nbytes / HBM_PEAK_GBS / 1e6, 4),
+                "eager_ms_per_token": round(ms_eager, 3), "context": ctx, "logits_finite": finite,
+                "timing": f"median of 5 x {reps} graph replays, hip events"}
+
     if args.gemm_only:
         print(json.dumps({"config4_gemm": gemm_set()}), flush=True)
+        return
+    if args.decode_only:
+        print(json.dumps({"config5_decode": decode_step()}), flush=True)
         return
 
     bytes_m1 = sum(synth.gemv_bytes(1, N, K, G) for _, N, K in layers)
@@ -256,6 +310,7 @@ def main():
         del c1w, wq0, s0
 
         extra["config4_gemm"] = gemm_set()
+        extra["config5_decode"] = decode_step()
 
 
     # ---------------- CPU baseline (PyTorch CPU dequant + fp32 matmul), full M=1 set

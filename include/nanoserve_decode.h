@@ -1,0 +1,92 @@
+/*
+ * nanoserve_decode.h -- C ABI of the operators around the W4 linear layers in one decoder
+ * step (libnanoserve_amd.so): the reference's fused residual-add + RMSNorm, RoPE and SwiGLU
+ * entry points, and the one-token attention step that the reference's runner does with
+ * PyTorch ops.
+ *
+ * Same conventions as nanoserve_w4.h: caller-allocated device memory, bf16 tensors passed as
+ * void* (row-major, 16-byte aligned where a kernel reads 16-byte vectors), `stream` a
+ * hipStream_t as void*, asynchronous, no allocation, no host synchronisation (every entry
+ * point may be captured in a HIP graph). Return codes: 0 on success, -1 / -2 for rejected
+ * arguments (checked before any HIP call), otherwise the hipError_t after the launch.
+ */
+#ifndef NANOSERVE_DECODE_H
+#define NANOSERVE_DECODE_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/*
+ * Replaces ns_rmsnorm (reference csrc/nanoserve_ops.cu:20-27; kernel
+ * kernels/fused/rmsnorm.cuh:1-52).
+ * x [T][H] residual stream; if r != NULL, x <- bf16_rne(x + r) in place (r [T][H]), else x
+ * is only read. y [T][H] = bf16_rne(x * rsqrt(mean(x^2) + eps) * w), w [H], fp32 arithmetic.
+ * Returns -1 for H % 8 != 0, H > 8192 (the reference's limit, where it calls exit()), T < 0,
+ * NULL x / w / y, or a pointer that is not 16-byte aligned. T == 0 is a no-op.
+ */
+int ns_rmsnorm(void* x, const void* r, const void* w, void* y, int T, int H, float eps,
+               void* stream);
+
+/*
+ * Replaces ns_rope (reference csrc/nanoserve_ops.cu:29-36; kernel kernels/fused/rope.cuh:1-46).
+ * In place on q [T][Hq][D] and k [T][Hk][D], token strides q_stride / k_stride in elements
+ * (negative: Hq*D / Hk*D). Token t is at position pos0 + t; for i < D/2, with
+ * a = fp32(pos0 + t) * inv_freq[i] (inv_freq [D/2] fp32):
+ *   x[i] <- x[i] cos a - x[i + D/2] sin a,   x[i + D/2] <- x[i + D/2] cos a + x[i] sin a.
+ * Returns -1 for D % 16 != 0, T < 0, Hq < 0, Hk < 0, strides not a multiple of 8, NULL or
+ * pointers not 16-byte aligned (q, k) / 4-byte aligned (inv_freq).
+ */
+int ns_rope(void* q, void* k, const void* inv_freq, int T, int Hq, int Hk, int D, int pos0,
+            long long q_stride, long long k_stride, void* stream);
+
+/*
+ * Replaces ns_swiglu (reference csrc/nanoserve_ops.cu:38-44; kernel kernels/fused/swiglu.cuh:
+ * 35-52). out [T][I] = bf16_rne(silu(gate) * up), gate and up contiguous [T][I],
+ * silu(g) = g / (1 + exp(-g)) in fp32. Returns -1 if T*I % 8 != 0 (as the reference), for
+ * negative sizes, NULL or pointers that are not 16-byte aligned.
+ */
+int ns_swiglu(const void* gate, const void* up, void* out, int T, int I, void* stream);
+
+/*
+ * No counterpart in the reference's C ABI: the reference does this step with PyTorch ops
+ * (python/nanoserve/qwen.py:147-151: bias add, rope, and the cache store of 119-122).
+ * One decode token: qkv [(Hq + 2 Hk) * D] bf16 is the fused projection output (q heads, then
+ * k heads, then v heads). In place: every element gets bf16_rne(qkv + bias) (bias NULL: no add), then q and k
+ * heads are rotated as by ns_rope at position *pos. The rotated k heads and the v heads are
+ * also written to k_cache / v_cache [Hk][max_len][D] at row *pos (one layer's slice of a
+ * [layers][Hk][max_len][D] cache). pos is a device int32 so that a captured graph can be
+ * replayed at any position; a position outside [0, max_len) writes no cache row.
+ * Returns -2 for D % 16 != 0, Hq <= 0, Hk <= 0, max_len <= 0, NULL or misaligned pointers.
+ */
+int ns_decode_qkv(void* qkv, const void* bias, const void* inv_freq, const int* pos,
+                  void* k_cache, void* v_cache, int Hq, int Hk, int D, int max_len,
+                  void* stream);
+
+/*
+ * Bytes of fp32 workspace ns_decode_attention needs for these sizes (partial results of the
+ * split over cache positions). 0 for invalid sizes.
+ */
+size_t ns_decode_attention_workspace(int Hq, int D, int max_len);
+
+/*
+ * No counterpart in the reference's C ABI: the reference's decode attention is PyTorch SDPA
+ * over the cache (python/nanoserve/qwen.py:124-133). One query token, grouped-query heads:
+ * out [Hq][D] bf16 = softmax(q_h . K_g^T / sqrt(D)) V_g over cache rows 0 .. n-1,
+ * n = min(*pos + 1, max_len), g = h / (Hq / Hk); q [Hq][D] bf16 (may be the q part of the
+ * ns_decode_qkv buffer), k_cache / v_cache [Hk][max_len][D] bf16, fp32 scores, softmax and
+ * accumulation. work: ns_decode_attention_workspace(Hq, D, max_len) bytes of device memory,
+ * overwritten. n <= 0 gives zeros. Returns -2 for D != 128, Hq % Hk != 0, Hq / Hk > 8,
+ * max_len <= 0, work_bytes too small, NULL or misaligned pointers.
+ */
+int ns_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* pos,
+                        void* out, void* work, size_t work_bytes, int Hq, int Hk, int D,
+                        int max_len, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOSERVE_DECODE_H */

@@ -15,12 +15,21 @@ import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnanoserve_amd.so")
 
-# Exported symbols and their ctypes signatures (include/nanoserve_w4.h).
-_VP, _I32 = ctypes.c_void_p, ctypes.c_int
+# Exported symbols and their ctypes signatures (include/nanoserve_w4.h,
+# include/nanoserve_decode.h); every function returns int except where RESTYPES says otherwise.
+_VP, _I32, _I64, _F32, _SZ = (ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_float,
+                              ctypes.c_size_t)
 SIGNATURES = {
     "ns_w4_quantize": [_VP, _VP, _VP, _I32, _I32, _I32, _VP],
     "ns_w4_linear": [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP],
+    "ns_rmsnorm": [_VP, _VP, _VP, _VP, _I32, _I32, _F32, _VP],
+    "ns_rope": [_VP, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I64, _I64, _VP],
+    "ns_swiglu": [_VP, _VP, _VP, _I32, _I32, _VP],
+    "ns_decode_qkv": [_VP, _VP, _VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP],
+    "ns_decode_attention_workspace": [_I32, _I32, _I32],
+    "ns_decode_attention": [_VP, _VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32, _I32, _VP],
 }
+RESTYPES = {"ns_decode_attention_workspace": _SZ}
 
 
 def _require_gpu_tensor(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
@@ -30,6 +39,13 @@ def _require_gpu_tensor(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
         raise ValueError(f"{name} must be a GPU tensor (got device {t.device})")
     if t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+
+
+def _check_out(out: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
+    _require_gpu_tensor(out, "out", like.dtype)
+    if out.shape != like.shape or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous tensor of shape {tuple(like.shape)}")
+    return out
 
 
 class Kernels:
@@ -44,7 +60,7 @@ class Kernels:
         for name, args in SIGNATURES.items():
             fn = getattr(self.lib, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
 
     # reference ops.py:32-34: the current torch stream (a hipStream_t on ROCm)
     @staticmethod
@@ -70,12 +86,13 @@ class Kernels:
         self._check(rc, "ns_w4_quantize")
         return Wq, S
 
-    def w4_linear(self, x, Wq, S, group=128):
+    def w4_linear(self, x, Wq, S, group=128, out=None):
         """x [M, K] bf16 -> y [M, N] bf16 = x @ deq(Wq, S)^T. Reference ops.py:85-97.
 
         M <= 8 runs natively (the reference pads 3 -> 4 and 5..7 -> 8 with zero rows, which
         does not change any output row); larger M is padded with zero rows up to a multiple
-        of 128, as the reference does."""
+        of 128, as the reference does. ``out`` (not in the reference): a contiguous [M, N]
+        bf16 tensor to write instead of a new one, for M that needs no padding."""
         _require_gpu_tensor(x, "x", torch.bfloat16)
         _require_gpu_tensor(Wq, "Wq", torch.int32)
         _require_gpu_tensor(S, "S", torch.bfloat16)
@@ -89,8 +106,107 @@ class Kernels:
         x = x.contiguous()
         Wq = Wq.contiguous()
         S = S.contiguous()
-        y = torch.empty((Mp, N), dtype=torch.bfloat16, device=x.device)
+        if out is not None:
+            _require_gpu_tensor(out, "out", torch.bfloat16)
+            if Mp != M or tuple(out.shape) != (M, N) or not out.is_contiguous():
+                raise ValueError(f"out must be a contiguous [{M}, {N}] tensor and M must need "
+                                 "no padding")
+            y = out
+        else:
+            y = torch.empty((Mp, N), dtype=torch.bfloat16, device=x.device)
         rc = self.lib.ns_w4_linear(x.data_ptr(), Wq.data_ptr(), S.data_ptr(), y.data_ptr(), Mp, N,
                                    K, group, self._stream())
         self._check(rc, "ns_w4_linear")
         return y[:M]
+
+    # ------------------------------------------------------------------ decoder-step operators
+    def rmsnorm(self, x, r, w, eps, out=None):
+        """x [T, H] residual stream, updated in place to x + r when r is given; returns
+        rmsnorm(x) * w. Reference ops.py:41-48 (kernel: kernels/fused/rmsnorm.cuh:10-52).
+        ``out`` (not in the reference): a contiguous tensor like x to write the result to."""
+        _require_gpu_tensor(x, "x", torch.bfloat16)
+        _require_gpu_tensor(w, "w", torch.bfloat16)
+        if not x.is_contiguous():
+            raise ValueError("x must be contiguous (it is updated in place)")
+        if r is not None:
+            _require_gpu_tensor(r, "r", torch.bfloat16)
+            r = r.contiguous()
+        y = torch.empty_like(x) if out is None else _check_out(out, x)
+        rc = self.lib.ns_rmsnorm(x.data_ptr(), None if r is None else r.data_ptr(),
+                                 w.contiguous().data_ptr(), y.data_ptr(), x.shape[0], x.shape[1],
+                                 eps, self._stream())
+        self._check(rc, "ns_rmsnorm")
+        return y
+
+    def rope(self, q, k, inv_freq, n_heads, n_kv_heads, head_dim, pos0):
+        """In place on q [T, Hq*D] and k [T, Hk*D] (row stride may exceed Hq*D / Hk*D).
+        Reference ops.py:50-54 (kernel: kernels/fused/rope.cuh:14-46)."""
+        _require_gpu_tensor(q, "q", torch.bfloat16)
+        _require_gpu_tensor(k, "k", torch.bfloat16)
+        _require_gpu_tensor(inv_freq, "inv_freq", torch.float32)
+        for t, n in ((q, "q"), (k, "k")):
+            if t.stride(-1) != 1:
+                raise ValueError(f"{n} rows must be contiguous")
+        rc = self.lib.ns_rope(q.data_ptr(), k.data_ptr(), inv_freq.contiguous().data_ptr(),
+                              q.shape[0], n_heads, n_kv_heads, head_dim, pos0, q.stride(0),
+                              k.stride(0), self._stream())
+        self._check(rc, "ns_rope")
+
+    def swiglu(self, gate, up, out=None):
+        """silu(gate) * up, gate and up contiguous [T, I]. Reference ops.py:56-62 (kernel:
+        kernels/fused/swiglu.cuh:35-52). ``out`` (not in the reference): a contiguous tensor
+        like gate to write the result to."""
+        _require_gpu_tensor(gate, "gate", torch.bfloat16)
+        _require_gpu_tensor(up, "up", torch.bfloat16)
+        if not (gate.is_contiguous() and up.is_contiguous()):
+            raise ValueError("gate and up must be contiguous")
+        out = torch.empty_like(gate) if out is None else _check_out(out, gate)
+        rc = self.lib.ns_swiglu(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.shape[0],
+                                gate.shape[1], self._stream())
+        self._check(rc, "ns_swiglu")
+        return out
+
+    def decode_qkv(self, qkv, bias, inv_freq, pos, k_cache, v_cache, n_heads, n_kv_heads,
+                   head_dim):
+        """One decode token: bias add + RoPE at position pos[0] (device int32) in place on the
+        fused projection output qkv [(Hq + 2Hk) * D], and the k / v heads appended to one
+        layer's cache slices k_cache / v_cache [Hk, max_len, D]. The reference does these
+        steps with PyTorch ops (qwen.py:119-122, 147-151)."""
+        _require_gpu_tensor(qkv, "qkv", torch.bfloat16)
+        _require_gpu_tensor(inv_freq, "inv_freq", torch.float32)
+        _require_gpu_tensor(pos, "pos", torch.int32)
+        for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+            _require_gpu_tensor(t, n, torch.bfloat16)
+            if not t.is_contiguous():
+                raise ValueError(f"{n} must be contiguous")
+        if bias is not None:
+            _require_gpu_tensor(bias, "bias", torch.bfloat16)
+        if not qkv.is_contiguous():
+            raise ValueError("qkv must be contiguous")
+        rc = self.lib.ns_decode_qkv(qkv.data_ptr(), None if bias is None else bias.data_ptr(),
+                                    inv_freq.data_ptr(), pos.data_ptr(), k_cache.data_ptr(),
+                                    v_cache.data_ptr(), n_heads, n_kv_heads, head_dim,
+                                    k_cache.shape[-2], self._stream())
+        self._check(rc, "ns_decode_qkv")
+
+    def decode_attention_workspace(self, n_heads, head_dim, max_len):
+        """Bytes of device workspace decode_attention needs."""
+        return int(self.lib.ns_decode_attention_workspace(n_heads, head_dim, max_len))
+
+    def decode_attention(self, q, k_cache, v_cache, pos, n_heads, n_kv_heads, head_dim,
+                         work, out=None):
+        """Attention of one query token q [Hq * D] over cache rows 0 .. pos[0] of one layer's
+        k_cache / v_cache [Hk, max_len, D]; returns out [1, Hq * D] bf16. The reference uses
+        PyTorch SDPA for this (qwen.py:124-133). work: a uint8 device tensor of at least
+        decode_attention_workspace(...) bytes."""
+        _require_gpu_tensor(q, "q", torch.bfloat16)
+        _require_gpu_tensor(pos, "pos", torch.int32)
+        _require_gpu_tensor(work, "work", torch.uint8)
+        if out is None:
+            out = torch.empty((1, n_heads * head_dim), dtype=torch.bfloat16, device=q.device)
+        rc = self.lib.ns_decode_attention(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                          pos.data_ptr(), out.data_ptr(), work.data_ptr(),
+                                          work.numel(), n_heads, n_kv_heads, head_dim,
+                                          k_cache.shape[-2], self._stream())
+        self._check(rc, "ns_decode_attention")
+        return out

@@ -1,0 +1,346 @@
+"""W4A16 Qwen2 decoder on the nanoserve_amd kernels: the caller of the W4 linear layers.
+
+Counterpart of the reference's ``Qwen2Runner`` (python/nanoserve/qwen.py:43-177) with its
+options fixed to the fast path (``w4=True``, fused norm / rope / swiglu kernels). Batch 1. Per
+layer, as the reference's forward (qwen.py:137-164):
+
+    h = norm(x)                                  (layer 0 only; later layers get it fused below)
+    q, k, v = h [Wq|Wk|Wv] + [bq|bk|bv];  rope(q, k)  (one fused W4 projection)
+    a = attention(q, cache);   x = x + a Wo;   h = norm_post(x)     <- fused add + norm
+    m = swiglu(h [Wg|Wu]) Wd;  x = x + m;      h = norm_next(x)     <- fused add + norm
+    logits = h lm_head^T                         (lm_head stays bf16, as in the reference)
+
+Two differences of layout, not of arithmetic: q/k/v and gate/up are each one W4 projection
+(quantization is per row and per 128-column group, so stacking rows before quantizing gives
+the same codes and scales as quantizing them one by one), and a one-token decode step runs
+on device-resident token id and position (``decode``), so the whole step is captured once as
+a HIP graph and replayed for every token (``capture_decode``).
+
+Kernels used per decode step and layer: ns_w4_linear x4, ns_decode_qkv (bias + RoPE + KV
+append), ns_decode_attention (grouped-query attention over the cache), ns_rmsnorm x2,
+ns_swiglu. The prompt pass (T > 1) uses ns_w4_linear (GEMM for T > 8), ns_rope, ns_rmsnorm,
+ns_swiglu, and fp32 PyTorch attention for the prompt's causal attention.
+
+No weights are downloaded: ``random`` builds a model of any Qwen2 shape with seeded random
+weights (quantized by ns_w4_quantize), ``from_hf`` quantizes a Hugging Face Qwen2 model's
+weights.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from .ops import Kernels
+
+
+@dataclass(frozen=True)
+class Qwen2Shape:
+    """Architecture sizes; defaults are Qwen2.5-7B (hidden 3584, 28 layers, 28 query / 4 kv
+    heads of 128, intermediate 18944, vocabulary 152064, rope theta 1e6)."""
+    layers: int = 28
+    hidden: int = 3584
+    heads: int = 28
+    kv_heads: int = 4
+    head_dim: int = 128
+    intermediate: int = 18944
+    vocab: int = 152064
+    eps: float = 1e-6
+    rope_theta: float = 1000000.0
+    qkv_bias: bool = True
+    group: int = 128
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+    def w4_bytes_per_layer(self) -> int:
+        """Bytes of int4 codes + bf16 scales one layer's four projections read."""
+        def lin(n, k):
+            return n * k // 2 + n * (k // self.group) * 2
+        H, I = self.hidden, self.intermediate
+        return (lin(self.qkv_rows, H) + lin(H, self.heads * self.head_dim) + lin(2 * I, H)
+                + lin(H, I))
+
+    def decode_bytes(self, context: int) -> int:
+        """Bytes one decode step must read at least: every W4 projection, the bf16 lm_head and
+        the KV cache rows of ``context`` positions (embedding row, norms and activations are
+        negligible and not counted)."""
+        kv = 2 * self.layers * self.kv_heads * context * self.head_dim * 2
+        return self.layers * self.w4_bytes_per_layer() + self.vocab * self.hidden * 2 + kv
+
+
+class Qwen2Runner:
+    """W4A16 Qwen2 runner. Build with ``random`` or ``from_hf``; ``forward`` / ``generate`` have
+    the reference's signatures and semantics (qwen.py:137-177)."""
+
+    def __init__(self, shape: Qwen2Shape, embed, final_norm, lm_head, layers,
+                 kernels: Kernels | None = None):
+        self.shape = shape
+        self.k = kernels or Kernels()
+        self.embed, self.final_norm, self.lm_head = embed, final_norm, lm_head
+        self.layers = layers
+        self.dev = embed.device
+        D = shape.head_dim
+        if shape.heads % shape.kv_heads:
+            raise ValueError("heads must be a multiple of kv_heads")
+        # reference qwen.py:64-65: theta^(-2i/D) in fp32 from int64 exponents
+        self.inv_freq = 1.0 / (shape.rope_theta ** (
+            torch.arange(0, D, 2, dtype=torch.int64, device=self.dev).float() / D))
+        self.cache_k = self.cache_v = None
+        self.max_len = 0
+        self.graph = None
+        # one-token decode state: device-resident token id and position, static activations
+        H, I = shape.hidden, shape.intermediate
+        bf = dict(dtype=torch.bfloat16, device=self.dev)
+        self.tok = torch.zeros(1, dtype=torch.int64, device=self.dev)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=self.dev)
+        self.x = torch.empty(1, H, **bf)
+        self.h = torch.empty(1, H, **bf)
+        self.o = torch.empty(1, H, **bf)
+        self.qkv = torch.empty(1, shape.qkv_rows, **bf)
+        self.attn = torch.empty(1, shape.heads * D, **bf)
+        self.gu = torch.empty(1, 2 * I, **bf)
+        self.act = torch.empty(1, I, **bf)
+        self.logits = torch.empty(1, shape.vocab, **bf)
+        self.work = None
+
+    # ------------------------------------------------------------------ construction
+    @classmethod
+    def random(cls, shape: Qwen2Shape = Qwen2Shape(), device="cuda", seed: int = 0,
+               std: float = 0.02, kernels: Kernels | None = None) -> "Qwen2Runner":
+        """Seeded random weights: linear and embedding weights N(0, std) in bf16, quantized with
+        ns_w4_quantize; biases N(0, std); norm weights 1 + N(0, 0.05)."""
+        k = kernels or Kernels()
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        bf = torch.bfloat16
+
+        def randn(*size, scale=std):
+            return (torch.randn(*size, generator=g, device=device) * scale).to(bf)
+
+        def norm_w():
+            return (1.0 + torch.randn(shape.hidden, generator=g, device=device) * 0.05).to(bf)
+
+        H, I, D = shape.hidden, shape.intermediate, shape.head_dim
+        layers = []
+        for _ in range(shape.layers):
+            L = {"ln_in": norm_w(), "ln_post": norm_w(),
+                 "bqkv": randn(shape.qkv_rows) if shape.qkv_bias else None}
+            for name, (n, kk) in (("wqkv", (shape.qkv_rows, H)), ("wo", (H, shape.heads * D)),
+                                  ("wgu", (2 * I, H)), ("wd", (H, I))):
+                W = randn(n, kk)
+                L[name] = k.w4_quantize(W, shape.group)
+                del W
+            layers.append(L)
+        embed = randn(shape.vocab, H)
+        lm_head = randn(shape.vocab, H)
+        return cls(shape, embed, norm_w(), lm_head, layers, k)
+
+    @classmethod
+    def from_hf(cls, hf_model, device="cuda", group: int = 128,
+                kernels: Kernels | None = None) -> "Qwen2Runner":
+        """Quantize a Hugging Face Qwen2ForCausalLM's weights (as the reference's
+        Qwen2Runner.__init__ + quantize, qwen.py:43-99; default, unscaled RoPE only)."""
+        cfg = hf_model.config
+        k = kernels or Kernels()
+        rs = getattr(cfg, "rope_scaling", None)
+        rp = getattr(cfg, "rope_parameters", None)
+        rs = rs if isinstance(rs, dict) else {}
+        rp = rp if isinstance(rp, dict) else {}
+        rope_type = rs.get("rope_type") or rs.get("type") or rp.get("rope_type") or "default"
+        if rope_type != "default":
+            raise NotImplementedError(f"rope_type {rope_type!r} is not supported")
+        theta = (rp.get("rope_theta") or rs.get("rope_theta") or getattr(cfg, "rope_theta", None)
+                 or 10000.0)
+        D = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        m = hf_model.model
+        at0 = m.layers[0].self_attn
+        shape = Qwen2Shape(layers=len(m.layers), hidden=cfg.hidden_size,
+                           heads=cfg.num_attention_heads, kv_heads=cfg.num_key_value_heads,
+                           head_dim=D, intermediate=cfg.intermediate_size,
+                           vocab=m.embed_tokens.weight.shape[0], eps=cfg.rms_norm_eps,
+                           rope_theta=float(theta), qkv_bias=at0.q_proj.bias is not None,
+                           group=group)
+
+        def bf(t):
+            return t.detach().to(device=device, dtype=torch.bfloat16).contiguous()
+
+        layers = []
+        for layer in m.layers:
+            at, mlp = layer.self_attn, layer.mlp
+            L = {"ln_in": bf(layer.input_layernorm.weight),
+                 "ln_post": bf(layer.post_attention_layernorm.weight),
+                 "bqkv": (bf(torch.cat([at.q_proj.bias, at.k_proj.bias, at.v_proj.bias]))
+                          if shape.qkv_bias else None)}
+            stacks = {"wqkv": [at.q_proj.weight, at.k_proj.weight, at.v_proj.weight],
+                      "wo": [at.o_proj.weight],
+                      "wgu": [mlp.gate_proj.weight, mlp.up_proj.weight],
+                      "wd": [mlp.down_proj.weight]}
+            for name, ws in stacks.items():
+                L[name] = k.w4_quantize(bf(torch.cat([w.detach() for w in ws])), group)
+            layers.append(L)
+        return cls(shape, bf(m.embed_tokens.weight), bf(m.norm.weight),
+                   bf(hf_model.lm_head.weight), layers, k)
+
+    # ------------------------------------------------------------------ cache
+    def alloc_cache(self, max_len: int):
+        """KV cache [layers, kv_heads, max_len, head_dim] bf16 for K and for V (reference
+        qwen.py:114-117), and the decode-attention workspace. Drops a captured graph."""
+        s = self.shape
+        shape = (s.layers, s.kv_heads, max_len, s.head_dim)
+        self.cache_k = torch.empty(shape, dtype=torch.bfloat16, device=self.dev)
+        self.cache_v = torch.empty_like(self.cache_k)
+        self.max_len = max_len
+        nbytes = self.k.decode_attention_workspace(s.heads, s.head_dim, max_len)
+        if nbytes == 0:
+            raise ValueError("decode attention supports head_dim 128 only")
+        self.work = torch.empty(nbytes, dtype=torch.uint8, device=self.dev)
+        self.graph = None
+
+    def _store_kv(self, li, k, v, pos0):
+        s = self.shape
+        T = k.shape[0]
+        self.cache_k[li, :, pos0:pos0 + T] = k.reshape(T, s.kv_heads, s.head_dim).transpose(0, 1)
+        self.cache_v[li, :, pos0:pos0 + T] = v.reshape(T, s.kv_heads, s.head_dim).transpose(0, 1)
+
+    # ------------------------------------------------------------------ one-token decode step
+    def _decode_body(self):
+        """One decode step on self.tok / self.pos (device tensors) into self.logits. Launches
+        only; no allocation, no host synchronisation, so it can be captured."""
+        s, k = self.shape, self.k
+        H, I, D, G = s.hidden, s.intermediate, s.head_dim, s.group
+        torch.index_select(self.embed, 0, self.tok, out=self.x)
+        k.rmsnorm(self.x, None, self.layers[0]["ln_in"], s.eps, out=self.h)
+        q = self.qkv[0, :s.heads * D]
+        for li, L in enumerate(self.layers):
+            k.w4_linear(self.h, *L["wqkv"], G, out=self.qkv)
+            k.decode_qkv(self.qkv[0], L["bqkv"], self.inv_freq, self.pos, self.cache_k[li],
+                         self.cache_v[li], s.heads, s.kv_heads, D)
+            k.decode_attention(q, self.cache_k[li], self.cache_v[li], self.pos, s.heads,
+                               s.kv_heads, D, self.work, out=self.attn)
+            k.w4_linear(self.attn, *L["wo"], G, out=self.o)
+            k.rmsnorm(self.x, self.o, L["ln_post"], s.eps, out=self.h)
+            k.w4_linear(self.h, *L["wgu"], G, out=self.gu)
+            k.swiglu(self.gu[:, :I], self.gu[:, I:], out=self.act)
+            k.w4_linear(self.act, *L["wd"], G, out=self.o)
+            nxt = self.layers[li + 1]["ln_in"] if li + 1 < len(self.layers) else self.final_norm
+            k.rmsnorm(self.x, self.o, nxt, s.eps, out=self.h)
+        torch.mm(self.h, self.lm_head.t(), out=self.logits)
+
+    def _set_step(self, token, pos: int):
+        if self.cache_k is None:
+            raise RuntimeError("alloc_cache first")
+        if not 0 <= pos < self.max_len:
+            raise ValueError(f"position {pos} outside the cache (max_len {self.max_len})")
+        if isinstance(token, torch.Tensor):
+            self.tok.copy_(token.reshape(1))
+        else:
+            self.tok.fill_(int(token))
+        self.pos.fill_(pos)
+
+    def capture_decode(self):
+        """Capture one decode step as a HIP graph (replayed by ``decode``). The warm-up runs
+        and the capture write cache row max_len - 1, which a step at that position rewrites
+        before reading it."""
+        if self.cache_k is None:
+            raise RuntimeError("alloc_cache first")
+        self.pos.fill_(self.max_len - 1)
+        side = torch.cuda.Stream(device=self.dev)
+        side.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                self._decode_body()
+        torch.cuda.current_stream(self.dev).wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._decode_body()
+        self.graph = g
+
+    @torch.no_grad()
+    def decode(self, token, pos: int) -> torch.Tensor:
+        """Logits [1, vocab] of one token at position ``pos``, attending over cache rows
+        0 .. pos (the token's own k / v are appended at row pos). Replays the captured graph
+        when there is one. Returns the runner's own logits buffer (overwritten by the next
+        step)."""
+        self._set_step(token, pos)
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self._decode_body()
+        return self.logits
+
+    # ------------------------------------------------------------------ prompt pass
+    def _prompt_attention(self, q, k, v, pos0, li):
+        """Causal attention of T query tokens at positions pos0 .. pos0+T-1 over cache / prompt
+        keys, in fp32 (PyTorch), returned as bf16 [T, Hq*D]."""
+        s = self.shape
+        T, D = q.shape[0], s.head_dim
+        rep = s.heads // s.kv_heads
+        qh = q.reshape(T, s.heads, D).transpose(0, 1).float().contiguous()
+        if pos0 == 0:
+            kh = k.reshape(T, s.kv_heads, D).transpose(0, 1).float()
+            vh = v.reshape(T, s.kv_heads, D).transpose(0, 1).float()
+        else:
+            kh = self.cache_k[li, :, :pos0 + T].float()
+            vh = self.cache_v[li, :, :pos0 + T].float()
+        kh = kh.repeat_interleave(rep, dim=0).contiguous()
+        vh = vh.repeat_interleave(rep, dim=0).contiguous()
+        n = kh.shape[1]
+        qpos = torch.arange(pos0, pos0 + T, device=q.device)[:, None]
+        mask = torch.arange(n, device=q.device)[None, :] <= qpos
+        o = F.scaled_dot_product_attention(qh[None], kh[None], vh[None], attn_mask=mask)
+        return o[0].transpose(0, 1).reshape(T, s.heads * D).to(torch.bfloat16)
+
+    @torch.no_grad()
+    def forward(self, ids, pos0: int = 0, use_cache: bool = False, last_only: bool = False):
+        """ids: [T] token ids at positions pos0 .. pos0+T-1; returns logits [T, vocab] (or
+        [1, vocab] with ``last_only``). Reference qwen.py:137-164. A one-token call with
+        pos0 > 0 is a decode step (cache required, its k / v row is always stored); other
+        calls attend causally over the prompt (and, for pos0 > 0, the cache)."""
+        s, k = self.shape, self.k
+        T = ids.shape[0]
+        if T == 1 and pos0 > 0:
+            logits = self.decode(ids.reshape(1), pos0)
+            return logits.clone()
+        if (use_cache or pos0 > 0) and (self.cache_k is None or pos0 + T > self.max_len):
+            raise RuntimeError("cache too small: alloc_cache(max_len) first")
+        H, I, D, G = s.hidden, s.intermediate, s.head_dim, s.group
+        qn, kn = s.heads * D, s.kv_heads * D
+        x = self.embed.index_select(0, ids.to(self.dev)).contiguous()
+        h = k.rmsnorm(x, None, self.layers[0]["ln_in"], s.eps)
+        for li, L in enumerate(self.layers):
+            qkv = k.w4_linear(h, *L["wqkv"], G)
+            if L["bqkv"] is not None:
+                qkv += L["bqkv"]
+            q, kk, v = qkv[:, :qn], qkv[:, qn:qn + kn], qkv[:, qn + kn:]
+            k.rope(q, kk, self.inv_freq, s.heads, s.kv_heads, D, pos0)
+            if use_cache or pos0 > 0:
+                self._store_kv(li, kk, v, pos0)
+            a = self._prompt_attention(q, kk, v, pos0, li)
+            h = k.rmsnorm(x, k.w4_linear(a, *L["wo"], G), L["ln_post"], s.eps)
+            gu = k.w4_linear(h, *L["wgu"], G)
+            act = k.swiglu(gu[:, :I].contiguous(), gu[:, I:].contiguous())
+            nxt = self.layers[li + 1]["ln_in"] if li + 1 < len(self.layers) else self.final_norm
+            h = k.rmsnorm(x, k.w4_linear(act, *L["wd"], G), nxt, s.eps)
+        if last_only:
+            h = h[-1:]
+        return F.linear(h, self.lm_head)
+
+    @torch.no_grad()
+    def generate(self, prompt_ids, n_new: int, use_graph: bool = True):
+        """Greedy decoding (reference qwen.py:166-177): returns the ``n_new`` generated ids. The
+        decode steps replay one captured graph when ``use_graph``."""
+        T = prompt_ids.shape[0]
+        self.alloc_cache(T + n_new)
+        if use_graph and n_new > 1:
+            self.capture_decode()
+        logits = self.forward(prompt_ids, 0, use_cache=True, last_only=True)
+        tok = logits[-1].argmax()
+        out = [tok]
+        for i in range(1, n_new):
+            logits = self.decode(tok, T + i - 1)
+            tok = logits[-1].argmax()
+            out.append(tok)
+        return [int(t) for t in out]

@@ -1,6 +1,6 @@
 """CPU-only checks of the C-ABI boundary (no GPU): the library loads without a GPU, exports
-exactly what include/nanoserve_w4.h declares, and rejects every invalid argument with the
-reference's return codes (csrc/nanoserve_ops.cu:65-90) before touching HIP."""
+exactly what include/*.h declare, and rejects every invalid argument with the reference's
+return codes (csrc/nanoserve_ops.cu:20-90) before touching HIP."""
 import ctypes
 import os
 import re
@@ -13,17 +13,28 @@ from nanoserve_amd import LIB_PATH, Kernels
 from nanoserve_amd.ops import SIGNATURES
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "nanoserve_w4.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("nanoserve_w4.h", "nanoserve_decode.h")]
 
 
 def declared_symbols():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\bint\s+(ns_\w+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(?:int|size_t)\s+(ns_\w+)\s*\(", text))
+    return sorted(names)
+
+
+def test_headers_are_all_listed():
+    assert sorted(os.listdir(os.path.join(ROOT, "include"))) == sorted(
+        os.path.basename(h) for h in HEADERS)
 
 
 def test_header_declares_the_reference_entry_points():
-    assert declared_symbols() == ["ns_w4_linear", "ns_w4_quantize"]
+    # the reference's W4 and fused-op entry points (csrc/nanoserve_ops.cu:20-90), plus the
+    # decode-step attention operators the reference does with PyTorch ops
+    assert declared_symbols() == sorted([
+        "ns_w4_linear", "ns_w4_quantize", "ns_rmsnorm", "ns_rope", "ns_swiglu",
+        "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -96,3 +107,56 @@ def test_python_wrapper_refuses_cpu_tensors(k):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(OSError):
         Kernels(str(tmp_path / "missing.so"))
+
+
+# ------------------------------------------------------------------ decoder-step operators
+def test_rmsnorm_rejects_bad_arguments(k):
+    assert k.lib.ns_rmsnorm(P, None, P, P, 1, 12, 1e-6, None) == -1        # H % 8
+    assert k.lib.ns_rmsnorm(P, None, P, P, 1, 8200, 1e-6, None) == -1      # H > 8192
+    assert k.lib.ns_rmsnorm(P, None, P, P, -1, 64, 1e-6, None) == -1
+    assert k.lib.ns_rmsnorm(None, None, P, P, 1, 64, 1e-6, None) == -1
+    assert k.lib.ns_rmsnorm(P + 2, None, P, P, 1, 64, 1e-6, None) == -1
+    assert k.lib.ns_rmsnorm(P, P + 8, P, P, 1, 64, 1e-6, None) == -1
+    assert k.lib.ns_rmsnorm(P, None, P, P, 0, 64, 1e-6, None) == 0
+
+
+def test_rope_rejects_bad_arguments(k):
+    assert k.lib.ns_rope(P, P, P, 1, 2, 1, 72, 0, -1, -1, None) == -1       # D % 16
+    assert k.lib.ns_rope(P, P, P, 1, 2, 1, 128, 0, 260, -1, None) == -1     # stride % 8
+    assert k.lib.ns_rope(P, P, P, -1, 2, 1, 128, 0, -1, -1, None) == -1
+    assert k.lib.ns_rope(None, P, P, 1, 2, 1, 128, 0, -1, -1, None) == -1
+    assert k.lib.ns_rope(P, P + 8, P, 1, 2, 1, 128, 0, -1, -1, None) == -1
+    assert k.lib.ns_rope(P, P, P, 0, 2, 1, 128, 0, -1, -1, None) == 0
+
+
+def test_swiglu_rejects_bad_arguments(k):
+    assert k.lib.ns_swiglu(P, P, P, 1, 12, None) == -1                      # T*I % 8
+    assert k.lib.ns_swiglu(P, P, P, -1, 8, None) == -1
+    assert k.lib.ns_swiglu(P, P + 4, P, 1, 8, None) == -1
+    assert k.lib.ns_swiglu(None, None, None, 0, 8, None) == 0
+
+
+def test_decode_qkv_rejects_bad_arguments(k):
+    assert k.lib.ns_decode_qkv(P, None, P, P, P, P, 28, 4, 72, 64, None) == -2
+    assert k.lib.ns_decode_qkv(P, None, P, P, P, P, 0, 4, 128, 64, None) == -2
+    assert k.lib.ns_decode_qkv(P, None, P, P, P, P, 28, 4, 128, 0, None) == -2
+    assert k.lib.ns_decode_qkv(P, None, P, None, P, P, 28, 4, 128, 64, None) == -2
+    assert k.lib.ns_decode_qkv(P, P + 2, P, P, P, P, 28, 4, 128, 64, None) == -2
+
+
+def test_decode_attention_workspace_and_rejects(k):
+    ws = k.lib.ns_decode_attention_workspace(28, 128, 1024)
+    assert ws == 16 * 28 * 130 * 4  # 64-row splits x heads x (D + max + sum) floats
+    assert k.lib.ns_decode_attention_workspace(28, 64, 1024) == 0
+    assert k.lib.ns_decode_attention_workspace(28, 128, 0) == 0
+
+    def call(work_bytes=ws, Hq=28, Hk=4, D=128, L=1024, q=P, work=P):
+        return k.lib.ns_decode_attention(q, P, P, P, P, work, work_bytes, Hq, Hk, D, L, None)
+
+    assert call(work_bytes=ws - 1) == -2
+    assert call(D=64) == -2
+    assert call(Hq=27) == -2                   # Hq % Hk
+    assert call(Hq=36, Hk=4) == -2             # more than 8 query heads per kv head
+    assert call(L=0) == -2
+    assert call(q=None) == -2
+    assert call(work=P + 4) == -2

@@ -1,0 +1,275 @@
+"""GPU parity of the decoder-step kernels (nanoserve_amd/csrc/decode_ops.hip) against the CPU
+oracle (oracle/decode_ref.py, pinned in tests/test_decode_oracle.py), and of the W4A16 Qwen2
+runner (nanoserve_amd/qwen.py) against Hugging Face transformers' Qwen2ForCausalLM evaluated
+in float32 on the CPU with the same (dequantized) weights.
+
+Tolerances, all stated against a float64 / float32 reference:
+  * bit-exact: residual-stream adds, bias adds, cache rows not written, v rows;
+  * bf16 outputs of fp32 arithmetic: rtol 2^-8 (half a bf16 ulp of rounding plus fp32 error)
+    with a small absolute floor;
+  * the whole runner: max |logits - ref| <= 3e-2 * max |ref| and cosine similarity >= 0.999
+    (bf16 activations between kernels, as the reference's runner; measured bf16-vs-fp32 gap
+    of the same models on the CPU: about 1e-2 * max |ref|);
+  * a replayed HIP graph equals the eager step bit for bit.
+"""
+import copy
+
+import pytest
+import torch
+
+from nanoserve_amd import Kernels
+from nanoserve_amd.qwen import Qwen2Runner, Qwen2Shape
+from oracle import decode_ref as R
+from oracle import w4_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def k():
+    return Kernels()
+
+
+def rnd(*shape, seed, scale=1.0, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype).to(DEV)
+
+
+def close(out, ref, rtol=2 ** -8, atol=1e-6):
+    torch.testing.assert_close(out.detach().double().cpu(), ref.double().cpu(), rtol=rtol,
+                               atol=atol)
+
+
+# ------------------------------------------------------------------ ns_rmsnorm
+@pytest.mark.parametrize("T,H", [(1, 3584), (4, 896), (33, 8), (2, 8192), (3, 4096)])
+@pytest.mark.parametrize("with_r", [False, True])
+def test_rmsnorm(k, T, H, with_r):
+    print(f"rmsnorm T={T} H={H} r={with_r}", flush=True)
+    x, r, w = rnd(T, H, seed=1, scale=3.0), rnd(T, H, seed=2), rnd(H, seed=3, scale=0.5)
+    x0 = x.clone()
+    y = k.rmsnorm(x, r if with_r else None, w, 1e-6)
+    torch.cuda.synchronize()
+    v_ref, y_ref = R.rmsnorm(x0, r if with_r else None, w, 1e-6)
+    assert torch.equal(x.double().cpu(), v_ref)  # residual stream: bit-exact
+    close(y, y_ref)
+
+
+def test_rmsnorm_rejects(k):
+    x = torch.empty(2, 12, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError):
+        k.rmsnorm(x, None, torch.empty(12, dtype=torch.bfloat16, device=DEV), 1e-6)
+
+
+# ------------------------------------------------------------------ ns_rope
+@pytest.mark.parametrize("T", [1, 5])
+@pytest.mark.parametrize("pos0", [0, 1023, 32000])
+def test_rope_in_fused_buffer(k, T, pos0):
+    print(f"rope T={T} pos0={pos0}", flush=True)
+    Hq, Hk, D = 28, 4, 128
+    qn, kn = Hq * D, Hk * D
+    qkv = rnd(T, qn + 2 * kn, seed=4, scale=2.0)
+    ref_in = qkv.clone()
+    freq = R.inv_freq(D, 1000000.0)
+    k.rope(qkv[:, :qn], qkv[:, qn:qn + kn], freq.to(DEV), Hq, Hk, D, pos0)
+    torch.cuda.synchronize()
+    pos = torch.arange(pos0, pos0 + T)
+    q_ref = R.rope(ref_in[:, :qn], Hq, D, pos, freq)
+    k_ref = R.rope(ref_in[:, qn:qn + kn], Hk, D, pos, freq)
+    close(qkv[:, :qn], q_ref, atol=1e-4)
+    close(qkv[:, qn:qn + kn], k_ref, atol=1e-4)
+    assert torch.equal(qkv[:, qn + kn:], ref_in[:, qn + kn:])  # v untouched
+
+
+# ------------------------------------------------------------------ ns_swiglu
+@pytest.mark.parametrize("T,I", [(1, 18944), (3, 1024), (1, 8), (7, 264)])
+def test_swiglu(k, T, I):
+    print(f"swiglu T={T} I={I}", flush=True)
+    g, u = rnd(T, I, seed=5, scale=4.0), rnd(T, I, seed=6)
+    out = k.swiglu(g, u)
+    torch.cuda.synchronize()
+    close(out, R.swiglu(g, u), atol=1e-6)
+
+
+# ------------------------------------------------------------------ ns_decode_qkv
+@pytest.mark.parametrize("pos", [0, 17, 63, 64, -1])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_decode_qkv(k, pos, with_bias):
+    print(f"decode_qkv pos={pos} bias={with_bias}", flush=True)
+    Hq, Hk, D, max_len = 28, 4, 128, 64
+    qn, kn = Hq * D, Hk * D
+    qkv = rnd(qn + 2 * kn, seed=7, scale=2.0)
+    bias = rnd(qn + 2 * kn, seed=8, scale=0.5) if with_bias else None
+    kc, vc = rnd(Hk, max_len, D, seed=9), rnd(Hk, max_len, D, seed=10)
+    qkv0, kc0, vc0 = qkv.clone(), kc.clone(), vc.clone()
+    freq = R.inv_freq(D, 1000000.0)
+    p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+    k.decode_qkv(qkv, bias, freq.to(DEV), p, kc, vc, Hq, Hk, D)
+    torch.cuda.synchronize()
+    q_ref, k_ref, v_ref = R.decode_qkv(qkv0, bias, Hq, Hk, D, pos, freq)
+    close(qkv[:qn], q_ref.reshape(-1), rtol=2 ** -7, atol=1e-4)
+    close(qkv[qn:qn + kn], k_ref.reshape(-1), rtol=2 ** -7, atol=1e-4)
+    assert torch.equal(qkv[qn + kn:].double().cpu(), v_ref.reshape(-1))
+    written = 0 <= pos < max_len
+    rows = torch.ones(max_len, dtype=torch.bool)
+    if written:
+        rows[pos] = False
+        assert torch.equal(kc[:, pos].reshape(-1), qkv[qn:qn + kn])
+        assert torch.equal(vc[:, pos].reshape(-1), qkv[qn + kn:])
+    assert torch.equal(kc[:, rows.to(DEV)], kc0[:, rows.to(DEV)])  # other rows untouched
+    assert torch.equal(vc[:, rows.to(DEV)], vc0[:, rows.to(DEV)])
+
+
+# ------------------------------------------------------------------ ns_decode_attention
+@pytest.mark.parametrize("Hq,Hk", [(28, 4), (7, 1), (4, 4), (8, 1), (16, 4)])
+@pytest.mark.parametrize("max_len,n", [(64, 1), (64, 64), (1024, 63), (1024, 65), (1024, 1024),
+                                       (1100, 1000), (1100, 1100)])
+def test_decode_attention(k, Hq, Hk, max_len, n):
+    print(f"decode_attention Hq={Hq} Hk={Hk} max_len={max_len} n={n}", flush=True)
+    D = 128
+    q = rnd(Hq * D, seed=11)
+    kc, vc = rnd(Hk, max_len, D, seed=12), rnd(Hk, max_len, D, seed=13)
+    work = torch.empty(k.decode_attention_workspace(Hq, D, max_len), dtype=torch.uint8,
+                       device=DEV)
+    p = torch.tensor([n - 1], dtype=torch.int32, device=DEV)
+    out = k.decode_attention(q, kc, vc, p, Hq, Hk, D, work)
+    torch.cuda.synchronize()
+    close(out.reshape(-1), R.decode_attention(q, kc, vc, n, Hq, Hk), atol=1e-5)
+
+
+def test_decode_attention_peaked_and_empty(k):
+    Hq, Hk, D, max_len = 28, 4, 128, 300
+    q = rnd(Hq * D, seed=14, scale=8.0)  # large logits: a few rows dominate each softmax
+    kc, vc = rnd(Hk, max_len, D, seed=15), rnd(Hk, max_len, D, seed=16)
+    work = torch.empty(k.decode_attention_workspace(Hq, D, max_len), dtype=torch.uint8,
+                       device=DEV)
+    p = torch.tensor([250], dtype=torch.int32, device=DEV)
+    out = k.decode_attention(q, kc, vc, p, Hq, Hk, D, work)
+    torch.cuda.synchronize()
+    close(out.reshape(-1), R.decode_attention(q, kc, vc, 251, Hq, Hk), atol=1e-5)
+    p.fill_(-1)  # no rows: zeros
+    out = k.decode_attention(q, kc, vc, p, Hq, Hk, D, work)
+    torch.cuda.synchronize()
+    assert not out.any()
+
+
+# ------------------------------------------------------------------ the runner
+def _hf_model(H, nh, nkv, I, V, layers, seed):
+    pytest.importorskip("transformers")
+    return R.tiny_qwen2(H, nh, nkv, I, V, layers, seed)
+
+
+def _effective_hf(m, runner):
+    """A float32 copy of the HF model holding exactly the weights the runner uses: W4 weights
+    dequantized by the oracle, everything else rounded to bf16."""
+    ref = copy.deepcopy(m)
+    s = runner.shape
+    D = s.head_dim
+    qn, kn, I = s.heads * D, s.kv_heads * D, s.intermediate
+
+    def deq(pair):
+        Wq, S = pair
+        return torch.from_numpy(O.dequant_f32(Wq.cpu().numpy().view("uint32"),
+                                              S.cpu().view(torch.int16).numpy().view("uint16"),
+                                              s.group))
+
+    def r16(t):
+        return t.detach().to(torch.bfloat16).float()
+
+    with torch.no_grad():
+        for layer, L in zip(ref.model.layers, runner.layers):
+            at, mlp = layer.self_attn, layer.mlp
+            wqkv = deq(L["wqkv"])
+            at.q_proj.weight.copy_(wqkv[:qn])
+            at.k_proj.weight.copy_(wqkv[qn:qn + kn])
+            at.v_proj.weight.copy_(wqkv[qn + kn:])
+            for b in (at.q_proj.bias, at.k_proj.bias, at.v_proj.bias):
+                b.copy_(r16(b))
+            at.o_proj.weight.copy_(deq(L["wo"]))
+            wgu = deq(L["wgu"])
+            mlp.gate_proj.weight.copy_(wgu[:I])
+            mlp.up_proj.weight.copy_(wgu[I:])
+            mlp.down_proj.weight.copy_(deq(L["wd"]))
+            for ln in (layer.input_layernorm, layer.post_attention_layernorm):
+                ln.weight.copy_(r16(ln.weight))
+        ref.model.norm.weight.copy_(r16(ref.model.norm.weight))
+        ref.model.embed_tokens.weight.copy_(r16(ref.model.embed_tokens.weight))
+        ref.lm_head.weight.copy_(r16(ref.lm_head.weight))
+    return ref
+
+
+def _check_logits(out, ref):
+    assert R.logits_match(out, ref), R.logits_gap(out, ref)
+
+
+@pytest.mark.parametrize("H,nh,nkv,I,V,T", [(896, 7, 1, 1024, 1000, 12),
+                                             (256, 2, 1, 512, 512, 5),
+                                             (512, 4, 2, 768, 640, 130)])
+def test_runner_matches_hf_qwen2(k, H, nh, nkv, I, V, T):
+    """Prompt pass (GEMV for T <= 8, GEMM above) and four decode steps, eager and graph."""
+    print(f"runner H={H} heads={nh}/{nkv} I={I} V={V} T={T}", flush=True)
+    m = _hf_model(H, nh, nkv, I, V, layers=2, seed=0)
+    runner = Qwen2Runner.from_hf(m, device=DEV, kernels=k)
+    ref_model = _effective_hf(m, runner)
+    n_dec = 4
+    ids = torch.randint(0, V, (T + n_dec,), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        ref = ref_model(ids[None]).logits[0]
+    runner.alloc_cache(T + n_dec)
+    prompt = runner.forward(ids[:T].to(DEV), 0, use_cache=True)
+    torch.cuda.synchronize()
+    _check_logits(prompt, ref[:T])
+    # eager decode steps, teacher-forced
+    eager = []
+    for i in range(n_dec):
+        eager.append(runner.forward(ids[T + i:T + i + 1].to(DEV), T + i, use_cache=True))
+    torch.cuda.synchronize()
+    for i in range(n_dec):
+        _check_logits(eager[i], ref[T + i:T + i + 1])
+    # the same steps through the captured graph: bit-identical to the eager steps
+    runner.capture_decode()
+    for i in range(n_dec):
+        out = runner.decode(ids[T + i].to(DEV), T + i).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[i]), i
+
+
+def test_graph_replays_match_eager_with_work_between(k):
+    """Several replays of one captured step at different positions, with eager kernel work and
+    synchronisations between them; every replay must equal the eager step."""
+    shape = Qwen2Shape(layers=2, hidden=896, heads=7, kv_heads=1, head_dim=128,
+                       intermediate=1024, vocab=1000)
+    runner = Qwen2Runner.random(shape, device=DEV, seed=3, kernels=k)
+    max_len = 200
+    runner.alloc_cache(max_len)
+    g = torch.Generator(device=DEV).manual_seed(4)
+    runner.cache_k.copy_(torch.randn(runner.cache_k.shape, generator=g, device=DEV))
+    runner.cache_v.copy_(torch.randn(runner.cache_v.shape, generator=g, device=DEV))
+    base_k, base_v = runner.cache_k.clone(), runner.cache_v.clone()
+    steps = [(5, 10), (17, 150), (999, 0), (3, 199)]
+    eager = []
+    for tok, pos in steps:
+        eager.append(runner.decode(tok, pos).clone())
+    torch.cuda.synchronize()
+    runner.cache_k.copy_(base_k)
+    runner.cache_v.copy_(base_v)
+    runner.capture_decode()
+    runner.cache_k.copy_(base_k)  # the capture wrote row max_len - 1
+    runner.cache_v.copy_(base_v)
+    for i, (tok, pos) in enumerate(steps):
+        junk = torch.randn(4096, device=DEV).sum()  # eager work between replays
+        out = runner.decode(tok, pos).clone()
+        torch.cuda.synchronize()
+        assert junk.isfinite()
+        assert torch.equal(out, eager[i]), (tok, pos)
+
+
+def test_generate_graph_equals_eager(k):
+    shape = Qwen2Shape(layers=2, hidden=256, heads=2, kv_heads=1, head_dim=128,
+                       intermediate=512, vocab=512)
+    runner = Qwen2Runner.random(shape, device=DEV, seed=5, kernels=k)
+    prompt = torch.randint(0, 512, (9,), generator=torch.Generator().manual_seed(6)).to(DEV)
+    a = runner.generate(prompt, 6, use_graph=False)
+    b = runner.generate(prompt, 6, use_graph=True)
+    assert a == b and len(a) == 6
