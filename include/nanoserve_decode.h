@@ -54,8 +54,8 @@ int ns_swiglu(const void* gate, const void* up, void* out, int T, int I, void* s
  * No counterpart in the reference's C ABI: the reference does this step with PyTorch ops
  * (python/nanoserve/qwen.py:147-151: bias add, rope, and the cache store of 119-122).
  * One decode token: qkv [(Hq + 2 Hk) * D] bf16 is the fused projection output (q heads, then
- * k heads, then v heads). In place: every element gets bf16_rne(qkv + bias) (bias NULL: no add), then q and k
- * heads are rotated as by ns_rope at position *pos. The rotated k heads and the v heads are
+ * k heads, then v heads). In place: every element gets bf16_rne(qkv + bias) (bias NULL: no
+ * add), then q and k heads are rotated as by ns_rope at position *pos. The rotated k heads and the v heads are
  * also written to k_cache / v_cache [Hk][max_len][D] at row *pos (one layer's slice of a
  * [layers][Hk][max_len][D] cache). pos is a device int32 so that a captured graph can be
  * replayed at any position; a position outside [0, max_len) writes no cache row.
@@ -66,24 +66,60 @@ int ns_decode_qkv(void* qkv, const void* bias, const void* inv_freq, const int* 
                   void* stream);
 
 /*
- * Bytes of fp32 workspace ns_decode_attention needs for these sizes (partial results of the
- * split over cache positions). 0 for invalid sizes.
+ * Bytes of device workspace that ns_decode_attention and ns_decode_qkv_attention need for
+ * these sizes: per-split partial results (fp32) of the split over cache rows. Launches that
+ * may overlap in time need workspaces of their own. 0 for invalid sizes.
  */
-size_t ns_decode_attention_workspace(int Hq, int D, int max_len);
+size_t ns_decode_attention_workspace(int Hq, int Hk, int D, int max_len);
 
 /*
  * No counterpart in the reference's C ABI: the reference's decode attention is PyTorch SDPA
  * over the cache (python/nanoserve/qwen.py:124-133). One query token, grouped-query heads:
  * out [Hq][D] bf16 = softmax(q_h . K_g^T / sqrt(D)) V_g over cache rows 0 .. n-1,
- * n = min(*pos + 1, max_len), g = h / (Hq / Hk); q [Hq][D] bf16 (may be the q part of the
- * ns_decode_qkv buffer), k_cache / v_cache [Hk][max_len][D] bf16, fp32 scores, softmax and
- * accumulation. work: ns_decode_attention_workspace(Hq, D, max_len) bytes of device memory,
- * overwritten. n <= 0 gives zeros. Returns -2 for D != 128, Hq % Hk != 0, Hq / Hk > 8,
- * max_len <= 0, work_bytes too small, NULL or misaligned pointers.
+ * n = min(*pos + 1, max_len), g = h / (Hq / Hk); q [Hq][D] bf16, k_cache / v_cache
+ * [Hk][max_len][D] bf16, fp32 scores, softmax and accumulation (the cache rows are split
+ * over workgroups; when there is more than one split a second kernel merges them). work:
+ * ns_decode_attention_workspace(...) bytes of device memory, overwritten.
+ * n <= 0 gives zeros. Returns -2 for D != 128, Hq % Hk != 0, Hq / Hk > 8, max_len <= 0,
+ * work_bytes too small, NULL or misaligned pointers.
  */
 int ns_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* pos,
                         void* out, void* work, size_t work_bytes, int Hq, int Hk, int D,
                         int max_len, void* stream);
+
+/*
+ * No counterpart in the reference's C ABI (its runner does these steps with PyTorch ops,
+ * python/nanoserve/qwen.py:119-133, 147-151). ns_decode_qkv followed by ns_decode_attention in
+ * one launch, without modifying qkv: the q heads get bias + RoPE at position *pos, the new k
+ * (bias + RoPE) and v (bias) rows are appended to the cache at row *pos, and out [Hq][D] is the
+ * attention of the rotated q over rows 0 .. min(*pos + 1, max_len) - 1. Same arguments,
+ * workspace and return codes as those two.
+ */
+int ns_decode_qkv_attention(const void* qkv, const void* bias, const void* inv_freq,
+                            const int* pos, void* k_cache, void* v_cache, void* out, void* work,
+                            size_t work_bytes, int Hq, int Hk, int D, int max_len,
+                            void* stream);
+
+/*
+ * No counterpart in the reference's C ABI: the decode-step GEMV (M = 1) with its neighbouring
+ * operators fused, for a one-token decoder step (the reference launches them one by one:
+ * python/nanoserve/qwen.py:145-162 with kernels/fused/rmsnorm.cuh and swiglu.cuh).
+ *   input:  res != NULL: the activation is rmsnorm(res + r) * norm_w, exactly as ns_rmsnorm
+ *           computes it (r may be NULL: rmsnorm(res) * norm_w); if res_out and r are not NULL,
+ *           res_out [K] receives the new residual stream bf16(res + r) (res_out must not alias
+ *           res or r). res == NULL: X [K] bf16 is the activation.
+ *   output: swiglu == 0: Y [N] bf16, as ns_w4_linear with M = 1.
+ *           swiglu != 0: the rows of Wq / S are gate and up rows interleaved in blocks of 8
+ *           (rows 16b .. 16b+7 = gate rows 8b .. 8b+7, rows 16b+8 .. 16b+15 = up rows
+ *           8b .. 8b+7); Y [N/2] = bf16(silu(g) * u) of the bf16 outputs g, u of each row pair,
+ *           as ns_swiglu over ns_w4_linear's output. Needs N % 16 == 0.
+ * Weight format as ns_w4_linear with G == 128. Returns -2 for G != 128, K % 128 != 0, K > 16384
+ * with res, N % 16 != 0 with swiglu, NULL or misaligned pointers (X, res, r, norm_w, res_out
+ * and Wq 16-byte aligned), res_out aliasing res or r.
+ */
+int ns_w4_gemv_decode(const void* X, const void* res, const void* r, const void* norm_w,
+                      float eps, void* res_out, const void* Wq, const void* S, void* Y, int N,
+                      int K, int G, int swiglu, void* stream);
 
 #ifdef __cplusplus
 }

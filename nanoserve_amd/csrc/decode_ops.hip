@@ -18,37 +18,6 @@ namespace {
 
 constexpr int kBlock = 256;
 
-__device__ __forceinline__ void unpack8(const u32x4_t& u, float (&f)[8]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = __uint_as_float(u[i] << 16);
-    f[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
-  }
-}
-
-__device__ __forceinline__ u32x4_t pack8(const float (&f)[8]) {
-  u32x4_t u;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) u[i] = pack_bf16x2_rne(f[2 * i], f[2 * i + 1]);
-  return u;
-}
-
-__device__ __forceinline__ float round_bf16(float f) {
-  return bf16_bits_to_f32(f32_to_bf16_rne(f));
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-  return v;
-}
-
 // ------------------------------------------------------------------ residual add + RMSNorm
 // One workgroup per row; each thread keeps up to MAXV 8-element vectors of the row in
 // registers between the sum of squares and the scaling, so x and r are read once.
@@ -150,7 +119,7 @@ __global__ void __launch_bounds__(kBlock)
     unpack8(gate[i], g);
     unpack8(up[i], u);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) g[e] = g[e] / (1.f + __expf(-g[e])) * u[e];
+    for (int e = 0; e < 8; ++e) g[e] = silu_mul(g[e], u[e]);
     out[i] = pack8(g);
   }
 }
@@ -220,167 +189,358 @@ __global__ void __launch_bounds__(kBlock)
 }
 
 // ------------------------------------------------------------------ decode attention
-// Split over cache rows: workgroup (s, g) covers rows [s*kChunk, (s+1)*kChunk) of kv head g
-// for all R = Hq/Hk query heads of the group (padded to RP). It writes, per query head, the
-// split's running max m (base-2 logits), sum l of 2^(logit - m) and the unnormalised output
-// sum_p 2^(logit_p - m) v_p (fp32); the combine kernel merges the splits.
+// Workgroup (s, g) covers cache rows [s*kChunk, (s+1)*kChunk) of kv head g for all R = Hq/Hk
+// query heads of the group. It computes the split's max m (base-2 logits), sum l of
+// 2^(logit - m) and unnormalised output sum_p 2^(logit_p - m) v_p in fp32. A single split
+// normalises and writes the output itself; otherwise the splits' partials go to the workspace
+// and a second kernel (decode_attn_merge_kernel) merges them; the kernel boundary orders the
+// partial stores before the merge's loads (an in-kernel merge by the last workgroup needs
+// device-scope fences, measured slower than the second launch).
 //
-// Scores: wave w takes rows 16w .. 16w+15 of the chunk, four lanes per row, each lane 32 of
-// the 128 dims (four 16-byte loads of its k row); the four partial dot products are summed
-// with two lane swaps. Values: wave w takes the same 16 rows, each lane two dims of a row
-// (one 4-byte load per row, the wave reads the 256-byte row whole); the four waves' partial
-// outputs are summed through LDS.
+// kFused: q is the fused projection output qkv [(Hq + 2Hk) * D]; every workgroup applies the
+// bias and RoPE to its group's q heads itself, and the workgroup whose split holds row *pos
+// also builds that row's k (bias + RoPE) and v (bias), appends both to the cache and takes
+// them from LDS (ns_decode_qkv followed by ns_decode_attention, in one launch).
+//
+// A kernel this small costs its memory round trips and its longest chain of dependent
+// instructions, so: every global load (k and v rows, q, bias) is issued at the start; the
+// scores of a wave's 16 rows x 16 query-head slots come from four v_mfma_f32_16x16x32_bf16
+// (A = k rows, lane l: row l%16, dims 32s + 8(l/16)..+7; B = q heads, lane l: head l%16, same
+// dims; D: lane l holds rows 4(l/16)+r of head l%16), so each lane owns one head and the
+// per-head max and sum need two lane swaps instead of a 64-lane reduction per head; the values
+// are a VALU loop, each lane two dims of each of the wave's rows (one 4-byte load per row: the
+// wave reads each 256-byte row whole), probabilities broadcast from LDS.
 constexpr int kChunk = 64;
 constexpr int kHeadDim = 128;
+constexpr int kMaxGroup = 8;  // query heads per kv head (score columns 0..7 of 16 used)
 
-template <int RP>
+template <bool kFused>
 __global__ void __launch_bounds__(kBlock)
-    decode_attn_partial_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-                               const uint16_t* __restrict__ vc, const int* __restrict__ pos_p,
-                               float* __restrict__ opart, float* __restrict__ ml, int Hq, int Hk,
-                               int max_len, float qscale) {
+    decode_attn_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ bias,
+                       const float* __restrict__ inv_freq, uint16_t* __restrict__ kc,
+                       uint16_t* __restrict__ vc, const int* __restrict__ pos_p,
+                       uint16_t* __restrict__ out, float* __restrict__ opart,
+                       float* __restrict__ ml, int Hq, int Hk, int max_len, float qscale) {
   constexpr int D = kHeadDim;
+  constexpr int RP = kMaxGroup;
   constexpr int NWV = kBlock / kWave;
-  __shared__ float qs[RP][D];
-  __shared__ float ps[kChunk][RP];
-  __shared__ float red[NWV][RP];
-  __shared__ float stat[2][RP];
+  constexpr int QS = D + 8;  // padded q row (bf16 elements)
+  __shared__ __attribute__((aligned(16))) uint16_t qb[16][QS];
+  __shared__ __attribute__((aligned(16))) float ps[kChunk][RP];
+  __shared__ float red_m[NWV][16];
+  __shared__ float red_l[NWV][16];
   __shared__ float ored[NWV][RP][D];
+  __shared__ float rot[2][D / 2];
+  __shared__ __attribute__((aligned(16))) uint16_t knew[D];
+  __shared__ __attribute__((aligned(16))) uint16_t vnew[D];
 
-  const int n = min(*pos_p + 1, max_len);
+  const int pos = *pos_p;
+  const int n = min(pos + 1, max_len);
   const int split = blockIdx.x, g = blockIdx.y;
+  const int R = Hq / Hk;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  if (n <= 0) {  // no rows: zeros (uniform over the workgroup)
+    if (split == 0)
+      for (int i = tid; i < R * D; i += kBlock) out[(size_t)g * R * D + i] = 0;
+    return;
+  }
   const int start = split * kChunk;
   if (start >= n) return;  // uniform over the workgroup
   const int cnt = min(kChunk, n - start);
-  const int R = Hq / Hk;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int nsplit = (n + kChunk - 1) / kChunk;
+  // row `pos` (the token's own) is in this split when it is in the cache at all
+  const bool has_new = kFused && pos < max_len && pos - start < kChunk;
 
-  for (int i = tid; i < RP * D; i += kBlock) {
-    const int h = i / D, d = i % D;
-    qs[h][d] = h < R ? bf16_bits_to_f32(q[(size_t)(g * R + h) * D + d]) * qscale : 0.f;
+  // ---- issue every load: k (MFMA A fragments), v (two dims per row), then q / bias
+  const int r16 = lane & 15, grp = lane >> 4;
+  const int krow = 16 * w + r16;  // this lane's k row within the chunk
+  const bool k_valid = krow < cnt;
+  const bool k_is_new = has_new && start + krow == pos;
+  u32x4_t ka[4] = {};
+  if (k_valid && !k_is_new) {
+    const uint16_t* src = kc + ((size_t)g * max_len + start + krow) * D + 8 * grp;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) ka[s4] = *reinterpret_cast<const u32x4_t*>(src + 32 * s4);
   }
-  __syncthreads();
-
-  // ---- scores (base-2 logits)
-  const int quarter = lane & 3;
-  const int pl = 16 * w + (lane >> 2);
-  const bool valid = pl < cnt;
-  float s[RP];
-#pragma unroll
-  for (int h = 0; h < RP; ++h) s[h] = 0.f;
-  if (valid) {
-    const u32x4_t* krow = reinterpret_cast<const u32x4_t*>(
-        kc + ((size_t)g * max_len + start + pl) * D + 32 * quarter);
-    u32x4_t kv[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) kv[j] = krow[j];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float kf[8];
-      unpack8(kv[j], kf);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = 32 * quarter + 8 * j + e;
-#pragma unroll
-        for (int h = 0; h < RP; ++h) s[h] = fmaf(kf[e], qs[h][d], s[h]);
-      }
-    }
-  }
-#pragma unroll
-  for (int h = 0; h < RP; ++h) {
-    s[h] += __shfl_xor(s[h], 1, kWave);
-    s[h] += __shfl_xor(s[h], 2, kWave);
-  }
-
-  // ---- max over the chunk
-#pragma unroll
-  for (int h = 0; h < RP; ++h) {
-    const float m = wave_max(valid ? s[h] : -INFINITY);
-    if (lane == 0) red[w][h] = m;
-  }
-  __syncthreads();
-  if (tid < RP) {
-    float m = red[0][tid];
-#pragma unroll
-    for (int i = 1; i < NWV; ++i) m = fmaxf(m, red[i][tid]);
-    stat[0][tid] = m;
-  }
-  __syncthreads();
-
-  // ---- probabilities and their sum (each row counted once, by its quarter-0 lane)
-#pragma unroll
-  for (int h = 0; h < RP; ++h) {
-    const float p = valid ? exp2f(s[h] - stat[0][h]) : 0.f;
-    if (valid && quarter == 0) ps[pl][h] = p;
-    const float l = wave_sum(quarter == 0 ? p : 0.f);
-    if (lane == 0) red[w][h] = l;
-  }
-  __syncthreads();
-  if (tid < RP) {
-    float l = 0.f;
-#pragma unroll
-    for (int i = 0; i < NWV; ++i) l += red[i][tid];
-    stat[1][tid] = l;
-  }
-
-  // ---- values
-  float acc[RP][2];
-#pragma unroll
-  for (int h = 0; h < RP; ++h) acc[h][0] = acc[h][1] = 0.f;
-  const uint16_t* vbase = vc + ((size_t)g * max_len + start) * D + 2 * lane;
   const int rows = min(16, cnt - 16 * w);
+  const uint16_t* vbase = vc + ((size_t)g * max_len + start + 16 * w) * D + 2 * lane;
   uint32_t vv[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
-    vv[i] = i < rows ? *reinterpret_cast<const uint32_t*>(vbase + (size_t)(16 * w + i) * D) : 0u;
+  for (int i = 0; i < 16; ++i) {
+    const bool v_is_new = has_new && start + 16 * w + i == pos;
+    vv[i] = i < rows && !v_is_new ? *reinterpret_cast<const uint32_t*>(vbase + (size_t)i * D) : 0u;
+  }
+
+  if constexpr (kFused) {
+    // thread t < 8R: q head t/8, rotation chunk pair t%8; then 8 threads for the k head's
+    // chunk pairs and 16 for the v head's chunks (only with has_new)
+    const int nq = 8 * R;
+    const bool is_q = tid < nq;
+    const bool is_k = has_new && tid >= nq && tid < nq + 8;
+    const bool is_v = has_new && tid >= nq + 8 && tid < nq + 24;
+    const int c = is_q ? tid % 8 : tid - nq;
+    u32x4_t a0{}, a1{}, b0{}, b1{};
+    if (is_q || is_k) {
+      const int off = (is_q ? g * R + tid / 8 : Hq + g) * D + 8 * c;
+      a0 = *reinterpret_cast<const u32x4_t*>(q + off);
+      a1 = *reinterpret_cast<const u32x4_t*>(q + off + D / 2);
+      if (bias) {
+        b0 = *reinterpret_cast<const u32x4_t*>(bias + off);
+        b1 = *reinterpret_cast<const u32x4_t*>(bias + off + D / 2);
+      }
+    } else if (is_v) {
+      const int off = (Hq + Hk + g) * D + 8 * (tid - nq - 8);
+      a0 = *reinterpret_cast<const u32x4_t*>(q + off);
+      if (bias) b0 = *reinterpret_cast<const u32x4_t*>(bias + off);
+    }
+    if (tid < D / 2) {  // the D/2 rotation angles of this position, once per workgroup
+      float sn, cs;
+      sincosf(static_cast<float>(pos) * inv_freq[tid], &sn, &cs);
+      rot[0][tid] = cs;
+      rot[1][tid] = sn;
+    }
+    if (tid >= nq && tid < 8 * 16) {  // zero q slots of heads R .. 15
+      const int h = tid / 8, cc = tid % 8;
+      *reinterpret_cast<u32x4_t*>(&qb[h][16 * cc]) = u32x4_t{};
+      *reinterpret_cast<u32x4_t*>(&qb[h][16 * cc + 8]) = u32x4_t{};
+    }
+    __syncthreads();
+    if (is_q || is_k) {
+      float lo[8], hi[8];
+      unpack8(a0, lo);
+      unpack8(a1, hi);
+      if (bias) {
+        float blo[8], bhi[8];
+        unpack8(b0, blo);
+        unpack8(b1, bhi);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          lo[e] = round_bf16(lo[e] + blo[e]);
+          hi[e] = round_bf16(hi[e] + bhi[e]);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float cs = rot[0][8 * c + e], sn = rot[1][8 * c + e];
+        const float x1 = lo[e], x2 = hi[e];
+        lo[e] = x1 * cs - x2 * sn;
+        hi[e] = x2 * cs + x1 * sn;
+      }
+      const u32x4_t plo = pack8(lo), phi = pack8(hi);
+      if (is_q) {
+        const int h = tid / 8;
+        *reinterpret_cast<u32x4_t*>(&qb[h][8 * c]) = plo;
+        *reinterpret_cast<u32x4_t*>(&qb[h][D / 2 + 8 * c]) = phi;
+      } else {
+        *reinterpret_cast<u32x4_t*>(&knew[8 * c]) = plo;
+        *reinterpret_cast<u32x4_t*>(&knew[D / 2 + 8 * c]) = phi;
+        uint16_t* row = kc + ((size_t)g * max_len + pos) * D;
+        *reinterpret_cast<u32x4_t*>(row + 8 * c) = plo;
+        *reinterpret_cast<u32x4_t*>(row + D / 2 + 8 * c) = phi;
+      }
+    } else if (is_v) {
+      u32x4_t v = a0;
+      if (bias) {
+        float x[8], b[8];
+        unpack8(a0, x);
+        unpack8(b0, b);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] += b[e];
+        v = pack8(x);
+      }
+      const int cv = tid - nq - 8;
+      *reinterpret_cast<u32x4_t*>(&vnew[8 * cv]) = v;
+      *reinterpret_cast<u32x4_t*>(vc + ((size_t)g * max_len + pos) * D + 8 * cv) = v;
+    }
+  } else {
+    if (tid < 8 * 16) {  // 16 dims per thread: two 16-byte loads
+      const int h = tid / 8, cc = tid % 8;
+      u32x4_t a0{}, a1{};
+      if (h < R) {
+        const uint16_t* src = q + (size_t)(g * R + h) * D + 16 * cc;
+        a0 = *reinterpret_cast<const u32x4_t*>(src);
+        a1 = *reinterpret_cast<const u32x4_t*>(src + 8);
+      }
+      *reinterpret_cast<u32x4_t*>(&qb[h][16 * cc]) = a0;
+      *reinterpret_cast<u32x4_t*>(&qb[h][16 * cc + 8]) = a1;
+    }
+  }
+  __syncthreads();
+  if (has_new) {  // the token's own row comes from LDS
+    if (k_is_new) {
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        ka[s4] = *reinterpret_cast<const u32x4_t*>(&knew[32 * s4 + 8 * grp]);
+    }
+    const int inew = pos - start - 16 * w;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (i == inew) vv[i] = *reinterpret_cast<const uint32_t*>(&vnew[2 * lane]);
+  }
+
+  // ---- scores: S[row][head] for the wave's 16 rows and 16 head slots
+  f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) {
+    const u32x4_t qf = *reinterpret_cast<const u32x4_t*>(&qb[r16][32 * s4 + 8 * grp]);
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka[s4]),
+                                                 __builtin_bit_cast(bf16x8_t, qf), sc, 0, 0, 0);
+  }
+  // lane: head h = r16, rows 16w + 4 grp + r (base-2 logits)
+  const int h = r16;
+  float sr[4];
+  float m = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const bool ok = 16 * w + 4 * grp + r < cnt;
+    sr[r] = ok ? sc[r] * qscale : -INFINITY;
+    m = fmaxf(m, sr[r]);
+  }
+  m = fmaxf(m, __shfl_xor(m, 16, kWave));
+  m = fmaxf(m, __shfl_xor(m, 32, kWave));
+  if (grp == 0) red_m[w][h] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red_m[0][h], red_m[1][h]), fmaxf(red_m[2][h], red_m[3][h]));
+  float l = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float p = exp2f(sr[r] - m);  // 0 for masked rows
+    l += p;
+    if (h < RP) ps[16 * w + 4 * grp + r][h] = p;
+  }
+  l += __shfl_xor(l, 16, kWave);
+  l += __shfl_xor(l, 32, kWave);
+  if (grp == 0) red_l[w][h] = l;
+  __syncthreads();
+
+  // ---- values: lane owns dims 2 lane, 2 lane + 1
+  float acc[RP][2];
+#pragma unroll
+  for (int hh = 0; hh < RP; ++hh) acc[hh][0] = acc[hh][1] = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     if (i < rows) {
       const float v0 = __uint_as_float(vv[i] << 16), v1 = __uint_as_float(vv[i] & 0xffff0000u);
+      const f32x4_t p0 = *reinterpret_cast<const f32x4_t*>(&ps[16 * w + i][0]);
+      const f32x4_t p1 = *reinterpret_cast<const f32x4_t*>(&ps[16 * w + i][4]);
 #pragma unroll
-      for (int h = 0; h < RP; ++h) {
-        const float p = ps[16 * w + i][h];
-        acc[h][0] = fmaf(p, v0, acc[h][0]);
-        acc[h][1] = fmaf(p, v1, acc[h][1]);
+      for (int hh = 0; hh < 4; ++hh) {
+        acc[hh][0] = fmaf(p0[hh], v0, acc[hh][0]);
+        acc[hh][1] = fmaf(p0[hh], v1, acc[hh][1]);
+        acc[hh + 4][0] = fmaf(p1[hh], v0, acc[hh + 4][0]);
+        acc[hh + 4][1] = fmaf(p1[hh], v1, acc[hh + 4][1]);
       }
     }
   }
 #pragma unroll
-  for (int h = 0; h < RP; ++h) {
-    ored[w][h][2 * lane] = acc[h][0];
-    ored[w][h][2 * lane + 1] = acc[h][1];
-  }
+  for (int hh = 0; hh < RP; ++hh)
+    *reinterpret_cast<float2*>(&ored[w][hh][2 * lane]) = make_float2(acc[hh][0], acc[hh][1]);
   __syncthreads();
+
+  const bool single = nsplit == 1;
   for (int i = tid; i < R * D; i += kBlock) {
-    const int h = i / D, d = i % D;
-    float o = 0.f;
-#pragma unroll
-    for (int k = 0; k < NWV; ++k) o += ored[k][h][d];
-    opart[((size_t)split * Hq + g * R + h) * D + d] = o;
+    const int hh = i / D, d = i % D;
+    const float o = (ored[0][hh][d] + ored[1][hh][d]) + (ored[2][hh][d] + ored[3][hh][d]);
+    if (single) {
+      const float lt = (red_l[0][hh] + red_l[1][hh]) + (red_l[2][hh] + red_l[3][hh]);
+      out[(size_t)(g * R + hh) * D + d] = static_cast<uint16_t>(f32_to_bf16_rne(o / lt));
+    } else {
+      opart[((size_t)split * Hq + g * R + hh) * D + d] = o;
+    }
   }
-  if (tid < R) {
-    ml[((size_t)split * Hq + g * R + tid) * 2] = stat[0][tid];
-    ml[((size_t)split * Hq + g * R + tid) * 2 + 1] = stat[1][tid];
+  if (!single && tid < R) {
+    const float mt = fmaxf(fmaxf(red_m[0][tid], red_m[1][tid]), fmaxf(red_m[2][tid], red_m[3][tid]));
+    const float lt = (red_l[0][tid] + red_l[1][tid]) + (red_l[2][tid] + red_l[3][tid]);
+    *reinterpret_cast<float2*>(&ml[((size_t)split * Hq + g * R + tid) * 2]) = make_float2(mt, lt);
   }
 }
 
-// One workgroup per query head, one thread per dim: merge the splits' partial softmaxes.
-__global__ void __launch_bounds__(kHeadDim)
-    decode_attn_combine_kernel(const float* __restrict__ opart, const float* __restrict__ ml,
-                               const int* __restrict__ pos_p, uint16_t* __restrict__ out, int Hq,
-                               int max_len) {
-  const int h = blockIdx.x, d = threadIdx.x;
+// Second launch: one workgroup per kv head merges the splits of its R query heads. Split
+// (max, sum) pairs go to LDS first, then every output element's split values are loaded in
+// batches of 16 splits, each batch issued before any is used.
+__global__ void __launch_bounds__(kBlock)
+    decode_attn_merge_kernel(const float* __restrict__ opart, const float* __restrict__ ml,
+                             const int* __restrict__ pos_p, uint16_t* __restrict__ out, int Hq,
+                             int Hk, int max_len) {
+  constexpr int D = kHeadDim;
+  constexpr int SB = 16;             // splits per load batch
+  constexpr int SMAX = 64;           // splits per LDS pass
+  __shared__ float wt[SMAX][kMaxGroup];
+  __shared__ float lsum[SMAX][kMaxGroup];
+  __shared__ float scale_old[kMaxGroup], inv_l[kMaxGroup];
   const int n = min(*pos_p + 1, max_len);
-  const int splits = n > 0 ? (n + kChunk - 1) / kChunk : 0;
-  float m = -INFINITY;
-  for (int s = 0; s < splits; ++s) m = fmaxf(m, ml[((size_t)s * Hq + h) * 2]);
-  float l = 0.f, o = 0.f;
-  for (int s = 0; s < splits; ++s) {
-    const float f = exp2f(ml[((size_t)s * Hq + h) * 2] - m);
-    l = fmaf(f, ml[((size_t)s * Hq + h) * 2 + 1], l);
-    o = fmaf(f, opart[((size_t)s * Hq + h) * kHeadDim + d], o);
+  const int nsplit = n > 0 ? (n + kChunk - 1) / kChunk : 0;
+  if (nsplit <= 1) return;  // written by the attention kernel itself
+  const int g = blockIdx.x, R = Hq / Hk, tid = threadIdx.x;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // outputs i = tid + 256k, k < 4 (R * D <= 1024)
+  float m_run = -INFINITY, l_run = 0.f;  // thread tid < R: head tid
+  for (int s0 = 0; s0 < nsplit; s0 += SMAX) {
+    const int ns = min(SMAX, nsplit - s0);
+    float2 st[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int i = tid + kBlock * k, sp = i / kMaxGroup, hh = i % kMaxGroup;
+      st[k] = sp < ns && hh < R
+                  ? *reinterpret_cast<const float2*>(&ml[((size_t)(s0 + sp) * Hq + g * R + hh) * 2])
+                  : make_float2(-INFINITY, 0.f);
+    }
+    __syncthreads();  // the previous pass is done with wt
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int i = tid + kBlock * k;
+      wt[i / kMaxGroup][i % kMaxGroup] = st[k].x;
+      lsum[i / kMaxGroup][i % kMaxGroup] = st[k].y;
+    }
+    __syncthreads();
+    if (tid < R) {
+      float mm = m_run;
+      for (int sp = 0; sp < ns; ++sp) mm = fmaxf(mm, wt[sp][tid]);
+      const float f_old = exp2f(m_run - mm);
+      float ll = l_run * f_old;
+      for (int sp = 0; sp < ns; ++sp) {
+        const float f = exp2f(wt[sp][tid] - mm);
+        ll = fmaf(f, lsum[sp][tid], ll);
+        wt[sp][tid] = f;
+      }
+      scale_old[tid] = f_old;
+      m_run = mm;
+      l_run = ll;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = tid + kBlock * k;
+      if (i < R * D) acc[k] *= scale_old[i / D];
+    }
+    for (int sb = 0; sb < ns; sb += SB) {
+      float v[4][SB];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = tid + kBlock * k;
+        const int hh = i / D, d = i % D;
+        const float* src = &opart[((size_t)(s0 + sb) * Hq + g * R + hh) * D + d];
+#pragma unroll
+        for (int u = 0; u < SB; ++u)
+          v[k][u] = i < R * D && sb + u < ns ? src[(size_t)u * Hq * D] : 0.f;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = tid + kBlock * k;
+        const int hh = min(i / D, kMaxGroup - 1);
+#pragma unroll
+        for (int u = 0; u < SB; ++u)
+          if (sb + u < ns) acc[k] = fmaf(wt[sb + u][hh], v[k][u], acc[k]);
+      }
+    }
   }
-  out[(size_t)h * kHeadDim + d] = static_cast<uint16_t>(f32_to_bf16_rne(splits ? o / l : 0.f));
+  if (tid < R) inv_l[tid] = 1.f / l_run;
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int i = tid + kBlock * k;
+    if (i < R * D)
+      out[(size_t)g * R * D + i] = static_cast<uint16_t>(f32_to_bf16_rne(acc[k] * inv_l[i / D]));
+  }
 }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -393,6 +553,42 @@ unsigned grid_for(size_t items) {
 }
 
 size_t attn_splits(int max_len) { return (static_cast<size_t>(max_len) + kChunk - 1) / kChunk; }
+
+// Workspace: split outputs [splits][Hq][D] and split (max, sum) pairs [splits][Hq][2], fp32.
+size_t attn_workspace(int Hq, int Hk, int D, int max_len) {
+  if (Hq <= 0 || Hk <= 0 || D != kHeadDim || max_len <= 0) return 0;
+  return attn_splits(max_len) * static_cast<size_t>(Hq) * (D + 2) * sizeof(float);
+}
+
+int attn_check(int Hq, int Hk, int D, int max_len, size_t work_bytes, const void* work) {
+  if (D != kHeadDim || Hq <= 0 || Hk <= 0 || Hq % Hk || Hq / Hk > 8 || max_len <= 0) return -2;
+  if (attn_splits(max_len) > 65535) return -2;
+  if (!work || !aligned(work, 16) || work_bytes < attn_workspace(Hq, Hk, D, max_len)) return -2;
+  return 0;
+}
+
+template <bool kFused>
+int launch_attn(const void* q, const void* bias, const void* inv_freq, void* kc, void* vc,
+                const int* pos, void* out, void* work, int Hq, int Hk, int max_len,
+                hipStream_t st) {
+  const size_t splits = attn_splits(max_len);
+  float* opart = static_cast<float*>(work);
+  float* ml = opart + splits * Hq * kHeadDim;
+  const float qscale = 1.4426950408889634f / sqrtf(static_cast<float>(kHeadDim));  // log2(e)/sqrt(D)
+  const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(Hk));
+  hipLaunchKernelGGL(decode_attn_kernel<kFused>, grid, dim3(kBlock), 0, st,
+                     static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(bias),
+                     static_cast<const float*>(inv_freq), static_cast<uint16_t*>(kc),
+                     static_cast<uint16_t*>(vc), pos, static_cast<uint16_t*>(out), opart, ml, Hq,
+                     Hk, max_len, qscale);
+  if (splits > 1) {
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return static_cast<int>(e);
+    hipLaunchKernelGGL(decode_attn_merge_kernel, dim3(Hk), dim3(kBlock), 0, st, opart, ml, pos,
+                       static_cast<uint16_t*>(out), Hq, Hk, max_len);
+  }
+  return last_status();
+}
 
 }  // namespace
 }  // namespace ns
@@ -463,43 +659,37 @@ int ns_decode_qkv(void* qkv, const void* bias, const void* inv_freq, const int* 
   return ns::last_status();
 }
 
-size_t ns_decode_attention_workspace(int Hq, int D, int max_len) {
-  if (Hq <= 0 || D != ns::kHeadDim || max_len <= 0) return 0;
-  return ns::attn_splits(max_len) * static_cast<size_t>(Hq) * (D + 2) * sizeof(float);
+size_t ns_decode_attention_workspace(int Hq, int Hk, int D, int max_len) {
+  return ns::attn_workspace(Hq, Hk, D, max_len);
 }
 
 int ns_decode_attention(const void* q, const void* k_cache, const void* v_cache, const int* pos,
                         void* out, void* work, size_t work_bytes, int Hq, int Hk, int D,
                         int max_len, void* stream) {
-  if (D != ns::kHeadDim || Hq <= 0 || Hk <= 0 || Hq % Hk || Hq / Hk > 8 || max_len <= 0)
-    return -2;
-  const size_t splits = ns::attn_splits(max_len);
-  if (splits > 65535) return -2;
-  if (work_bytes < ns_decode_attention_workspace(Hq, D, max_len)) return -2;
-  if (!q || !k_cache || !v_cache || !pos || !out || !work) return -2;
+  const int rc = ns::attn_check(Hq, Hk, D, max_len, work_bytes, work);
+  if (rc) return rc;
+  if (!q || !k_cache || !v_cache || !pos || !out) return -2;
   if (!ns::aligned(q, 16) || !ns::aligned(k_cache, 16) || !ns::aligned(v_cache, 16) ||
-      !ns::aligned(pos, 4) || !ns::aligned(out, 2) || !ns::aligned(work, 16))
+      !ns::aligned(pos, 4) || !ns::aligned(out, 2))
     return -2;
-  float* opart = static_cast<float*>(work);
-  float* ml = opart + splits * Hq * D;
-  const float qscale = 1.4426950408889634f / sqrtf(static_cast<float>(D));  // log2(e)/sqrt(D)
-  const auto st = static_cast<hipStream_t>(stream);
-  const auto qq = static_cast<const uint16_t*>(q);
-  const auto kc = static_cast<const uint16_t*>(k_cache);
-  const auto vc = static_cast<const uint16_t*>(v_cache);
-  const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(Hk));
-  const int R = Hq / Hk;
-  if (R <= 4)
-    hipLaunchKernelGGL(ns::decode_attn_partial_kernel<4>, grid, dim3(ns::kBlock), 0, st, qq, kc,
-                       vc, pos, opart, ml, Hq, Hk, max_len, qscale);
-  else
-    hipLaunchKernelGGL(ns::decode_attn_partial_kernel<8>, grid, dim3(ns::kBlock), 0, st, qq, kc,
-                       vc, pos, opart, ml, Hq, Hk, max_len, qscale);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return static_cast<int>(e);
-  hipLaunchKernelGGL(ns::decode_attn_combine_kernel, dim3(Hq), dim3(ns::kHeadDim), 0, st, opart,
-                     ml, pos, static_cast<uint16_t*>(out), Hq, max_len);
-  return ns::last_status();
+  return ns::launch_attn<false>(q, nullptr, nullptr, const_cast<void*>(k_cache),
+                                const_cast<void*>(v_cache), pos, out, work, Hq, Hk, max_len,
+                                static_cast<hipStream_t>(stream));
+}
+
+int ns_decode_qkv_attention(const void* qkv, const void* bias, const void* inv_freq,
+                            const int* pos, void* k_cache, void* v_cache, void* out, void* work,
+                            size_t work_bytes, int Hq, int Hk, int D, int max_len,
+                            void* stream) {
+  const int rc = ns::attn_check(Hq, Hk, D, max_len, work_bytes, work);
+  if (rc) return rc;
+  if (!qkv || !inv_freq || !pos || !k_cache || !v_cache || !out) return -2;
+  if (!ns::aligned(qkv, 16) || !ns::aligned(bias, 16) || !ns::aligned(inv_freq, 4) ||
+      !ns::aligned(pos, 4) || !ns::aligned(k_cache, 16) || !ns::aligned(v_cache, 16) ||
+      !ns::aligned(out, 2))
+    return -2;
+  return ns::launch_attn<true>(qkv, bias, inv_freq, k_cache, v_cache, pos, out, work, Hq, Hk,
+                               max_len, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

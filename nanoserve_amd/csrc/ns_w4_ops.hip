@@ -5,6 +5,7 @@
 // tested) on a machine without a GPU; HIP itself initialises lazily on the first launch.
 #include <stdint.h>
 
+#include "../../include/nanoserve_decode.h"
 #include "../../include/nanoserve_w4.h"
 #include "w4_kernels.h"
 
@@ -52,6 +53,32 @@ int ns_w4_linear(const void* X, const void* Wq, const void* S, void* Y, int M, i
   } else {
     return -2;
   }
+  if (e != hipSuccess) return static_cast<int>(e);
+  return last_status();
+}
+
+int ns_w4_gemv_decode(const void* X, const void* res, const void* r, const void* norm_w,
+                      float eps, void* res_out, const void* Wq, const void* S, void* Y, int N,
+                      int K, int G, int swiglu, void* stream) {
+  if (N <= 0 || K <= 0 || G != 128 || K % 128 || (res && K > 16384)) return -2;
+  if (!Wq || !S || !Y || (!res && !X) || (res && !norm_w)) return -2;
+  if (!aligned(Wq, 16) || !aligned(S, 2) || !aligned(Y, 2) || !aligned(X, 16) ||
+      !aligned(res, 16) || !aligned(r, 16) || !aligned(norm_w, 16) || !aligned(res_out, 16))
+    return -2;
+  if (res_out && (res_out == res || res_out == r)) return -2;
+  const ns::GemvArgs a{static_cast<const uint16_t*>(X), static_cast<const uint32_t*>(Wq),
+                       static_cast<const uint16_t*>(S), static_cast<uint16_t*>(Y), 1, N, K, G};
+  ns::M1Fuse fz;
+  fz.res = static_cast<const uint16_t*>(res);
+  fz.radd = static_cast<const uint16_t*>(r);
+  fz.nw = static_cast<const uint16_t*>(norm_w);
+  fz.res_out = static_cast<uint16_t*>(res_out);
+  fz.eps = eps;
+  int reject = 0;
+  const hipError_t e = ns::launch_gemv_fused(a, ns::gemv_plan(1, N, K, G), fz, res != nullptr,
+                                             swiglu != 0, static_cast<hipStream_t>(stream),
+                                             &reject);
+  if (reject) return -2;
   if (e != hipSuccess) return static_cast<int>(e);
   return last_status();
 }

@@ -56,4 +56,39 @@ __device__ __forceinline__ void unpack_word_128q(uint32_t w, uint32_t (&d)[4]) {
   }
 }
 
+// Eight bf16 (one 16-byte vector, element 2i in the low half of word i) <-> fp32.
+__device__ __forceinline__ void unpack8(const u32x4_t& u, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(u[i] << 16);
+    f[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ u32x4_t pack8(const float (&f)[8]) {
+  u32x4_t u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) u[i] = pack_bf16x2_rne(f[2 * i], f[2 * i + 1]);
+  return u;
+}
+
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_bits_to_f32(f32_to_bf16_rne(f));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// silu(g) * u, the reference's SwiGLU (kernels/fused/swiglu.cuh:8), in fp32.
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.f + __expf(-g)) * u; }
+
 }  // namespace ns

@@ -409,10 +409,10 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
 //  * Branch-free inner loop: the per-chunk offsets are stored four times (one 16-byte LDS read
 //    initialises the whole MFMA accumulator), the diagonal value is picked with three selects,
 //    and lanes off the diagonal (or on a padded slot) write to a private dummy slot.
-template <int NW, int R, int GR>
+template <int NW, int R, int GR, int XM, int YM, int XV>
 __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
-    const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int N, int K) {
+    const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int N, int K, M1Fuse fz) {
   constexpr uint32_t kOOB = 0x7fffffc0u;
   constexpr int XR = 136;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -452,16 +452,93 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     }
   };
 
+  // The activation's loads go first: the counter the compiler waits on completes in issue
+  // order, so loads issued after the weight ring would wait for the ring's HBM latency too.
+  // Buffer loads past the end of a vector return zeros (the K -> 16 CP padding), branch-free.
+  constexpr int NT = NW * kWave;
+  auto vec_rsrc = [&](const void* p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, K * 2, 0x00020000);
+  };
+  auto vec_load = [&](__amdgpu_buffer_rsrc_t r, int e) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, 16u * e, 0, 0));
+  };
+  u32x4_t xa[XV], xb[XV], xw[XV];
+  if constexpr (XM == kXPlain) {
+    const auto rx = vec_rsrc(X);
+#pragma unroll
+    for (int i = 0; i < XV; ++i) xa[i] = vec_load(rx, tid + i * NT);
+  } else {
+    const auto rr = vec_rsrc(fz.res), rw = vec_rsrc(fz.nw);
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      xa[i] = vec_load(rr, tid + i * NT);
+      xw[i] = vec_load(rw, tid + i * NT);
+    }
+    if constexpr (XM == kXNormAdd) {
+      const auto ra = vec_rsrc(fz.radd);
+#pragma unroll
+      for (int i = 0; i < XV; ++i) xb[i] = vec_load(ra, tid + i * NT);
+    }
+  }
+
   u32x4_t ring[R];
   uint32_t rsc[R];
 #pragma unroll
   for (int u = 0; u < R; ++u) issue(ring[u], rsc[u]);
   __builtin_amdgcn_sched_barrier(0);
 
-  const u32x4_t* x4 = reinterpret_cast<const u32x4_t*>(X);
-  for (int e = tid; e < 16 * CP; e += NW * kWave)
-    *reinterpret_cast<u32x4_t*>(&xl[(e >> 4) * XR + 8 * (e & 15)]) =
-        e < KV ? pair_order(x4[e]) : u32x4_t{0u, 0u, 0u, 0u};
+  if constexpr (XM != kXPlain) {
+    // x = rmsnorm(res + radd) * nw, as the fused RMSNorm kernel: residual rounded to bf16,
+    // sum of squares over the row (wave sums, then the workgroup's in LDS), one bf16 rounding
+    // of v * inv * w; one workgroup also stores the new residual stream.
+    __shared__ float nred[NW];
+    u32x4_t* o4 = blockIdx.x == 0 ? reinterpret_cast<u32x4_t*>(fz.res_out) : nullptr;
+    float v[XV][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      const int e = tid + i * NT;
+      unpack8(xa[i], v[i]);  // zeros past the row: they add nothing
+      if constexpr (XM == kXNormAdd) {
+        float b[8];
+        unpack8(xb[i], b);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[i][q] = round_bf16(v[i][q] + b[q]);
+        if (o4 && e < KV) o4[e] = pack8(v[i]);
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) ss = fmaf(v[i][q], v[i][q], ss);
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) nred[wv] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) tot += nred[i];
+    const float inv = rsqrtf(tot / static_cast<float>(K) + fz.eps);
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      const int e = tid + i * NT;
+      if (e < 16 * CP) {
+        float g[8], o[8];
+        unpack8(xw[i], g);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) o[q] = v[i][q] * inv * g[q];
+        *reinterpret_cast<u32x4_t*>(&xl[(e >> 4) * XR + 8 * (e & 15)]) = pair_order(pack8(o));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      const int e = tid + i * NT;
+      if (e < 16 * CP) *reinterpret_cast<u32x4_t*>(&xl[(e >> 4) * XR + 8 * (e & 15)]) = pair_order(xa[i]);
+    }
+    // rows longer than XV vectors per thread (K > 8 XV NT): the rest, loaded here
+    const u32x4_t* x4 = reinterpret_cast<const u32x4_t*>(X);
+    for (int e = tid + XV * NT; e < 16 * CP; e += NT)
+      *reinterpret_cast<u32x4_t*>(&xl[(e >> 4) * XR + 8 * (e & 15)]) =
+          e < KV ? pair_order(x4[e]) : u32x4_t{0u, 0u, 0u, 0u};
+  }
   __syncthreads();
   const u32x4_t kNeg136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
   for (int cg = 16 * wv; cg < CP; cg += 16 * NW) {
@@ -519,8 +596,18 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
         for (int cc = kg; cc < C; cc += 4) v += pr[j * C + cc];
       v += __shfl_xor(v, 16, kWave);
       v += __shfl_xor(v, 32, kWave);
-      const int n = GR * g + j;
-      if (kg == 0 && j < GR && n < N) Y[n] = (uint16_t)f32_to_bf16_rne(v);
+      if constexpr (YM == kYSwiglu) {
+        // rows 16g..16g+7 are gate rows 8g.., rows 16g+8.. the matching up rows: the bf16
+        // outputs of row j and row j + 8 give activation 8g + j
+        static_assert(GR == 16, "SwiGLU output needs 16-row groups");
+        const float y = round_bf16(v);
+        const float up = __shfl_xor(y, 8, kWave);
+        const int n = 8 * g + j;
+        if (kg == 0 && j < 8 && 16 * g + j < N) Y[n] = (uint16_t)f32_to_bf16_rne(silu_mul(y, up));
+      } else {
+        const int n = GR * g + j;
+        if (kg == 0 && j < GR && n < N) Y[n] = (uint16_t)f32_to_bf16_rne(v);
+      }
     }
   }
 }
@@ -793,11 +880,12 @@ hipError_t launch_xlds(const GemvArgs& a, hipStream_t st) {
   return hipSuccess;
 }
 
-template <int NW, int R, int GR>
-hipError_t launch_m1(const GemvArgs& a, hipStream_t st) {
-  const void* fn = reinterpret_cast<const void*>(&w4_gemv_m1_kernel<NW, R, GR>);
+template <int NW, int R, int GR, int XM = kXPlain, int YM = kYPlain, int XV = kXVecs>
+hipError_t launch_m1(const GemvArgs& a, hipStream_t st, const M1Fuse& fz = M1Fuse{}) {
+  const void* fn = reinterpret_cast<const void*>(&w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV>);
+  // the planner keeps the dynamic part under 96 KiB; the limit leaves room for static LDS
   static const hipError_t attr =
-      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
   if (attr != hipSuccess) return attr;
   const size_t lds = m1_bytes(a.K, GR);
   int per_cu = 0;
@@ -809,8 +897,8 @@ hipError_t launch_m1(const GemvArgs& a, hipStream_t st) {
   // Two workgroups per CU: more resident waves only lengthen the memory queues.
   const int ngroups = (a.N + GR - 1) / GR;
   const int grid = max(1, min(ngroups, min(max(per_cu, 1), 2) * cus));
-  hipLaunchKernelGGL((w4_gemv_m1_kernel<NW, R, GR>), dim3(grid), dim3(NW * kWave), lds, st, a.X, a.Wq,
-                     a.S, a.Y, a.N, a.K);
+  hipLaunchKernelGGL((w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV>), dim3(grid), dim3(NW * kWave), lds, st,
+                     a.X, a.Wq, a.S, a.Y, a.N, a.K, fz);
   return hipSuccess;
 }
 
@@ -933,6 +1021,54 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
   NS_GEMV_CASE(2, 8)
 #undef NS_GEMV_CASE
   return hipErrorInvalidValue;
+}
+
+
+namespace {
+
+// The norm prologue keeps its vectors live across the row reduction, so it is compiled for
+// as few vectors per thread as the row needs (registers decide how many workgroups fit a CU).
+template <int NW, int GR, int YM, int XV>
+hipError_t launch_m1_norm(const GemvArgs& a, const M1Fuse& fz, hipStream_t st) {
+  if (fz.radd) return launch_m1<NW, 2, GR, kXNormAdd, YM, XV>(a, st, fz);
+  return launch_m1<NW, 2, GR, kXNorm, YM, XV>(a, st, fz);
+}
+
+template <int NW, int GR, int YM>
+hipError_t launch_m1_x(const GemvArgs& a, const M1Fuse& fz, bool norm, hipStream_t st) {
+  if (!norm) return launch_m1<NW, 2, GR, kXPlain, YM>(a, st, fz);
+  const int C = a.K >> 7, nvec = 16 * ((C + 15) & ~15);
+  if (nvec <= NW * kWave) return launch_m1_norm<NW, GR, YM, 1>(a, fz, st);
+  if (nvec <= 2 * NW * kWave) return launch_m1_norm<NW, GR, YM, 2>(a, fz, st);
+  return launch_m1_norm<NW, GR, YM, 4>(a, fz, st);
+}
+
+template <int NW, int GR>
+hipError_t launch_m1_fused(const GemvArgs& a, const M1Fuse& fz, bool norm, bool swiglu,
+                           hipStream_t st) {
+  if (swiglu) return launch_m1_x<NW, GR, kYSwiglu>(a, fz, norm, st);
+  return launch_m1_x<NW, GR, kYPlain>(a, fz, norm, st);
+}
+
+}  // namespace
+
+hipError_t launch_gemv_fused(const GemvArgs& a, const GemvPlan& p, const M1Fuse& fz, bool norm,
+                             bool swiglu, hipStream_t st, int* reject) {
+  *reject = 0;
+  const int C = a.K >> 7, CP = (C + 15) & ~15;
+  if (!p.m1 || p.rt != 2 || (swiglu && a.N % 16) ||
+      (norm && 16 * CP > kXVecs * p.nw * kWave)) {
+    *reject = 1;
+    return hipSuccess;
+  }
+  // the SwiGLU pairing needs 16-row groups
+  const int gr = swiglu ? 16 : p.gr;
+  if (p.nw == 16 && gr == 16) return launch_m1_fused<16, 16>(a, fz, norm, swiglu, st);
+  if (p.nw == 14 && gr == 16) return launch_m1_fused<14, 16>(a, fz, norm, swiglu, st);
+  if (p.nw == 8 && gr == 16) return launch_m1_fused<8, 16>(a, fz, norm, swiglu, st);
+  if (p.nw == 8 && gr == 8 && !swiglu) return launch_m1_x<8, 8, kYPlain>(a, fz, norm, st);
+  *reject = 1;
+  return hipSuccess;
 }
 
 }  // namespace ns

@@ -28,6 +28,26 @@ bool gemv_fast_path_ok(int M, int N, int K, int G);
 GemvPlan gemv_plan(int M, int N, int K, int G);
 hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st);
 
+// Neighbouring operators fused into the M = 1 GEMV (w4_gemv_m1_kernel):
+//   XM == kXNorm:    the activation is rmsnorm(res) * nw;
+//   XM == kXNormAdd: the activation is rmsnorm(res + radd) * nw; workgroup 0 stores
+//                    bf16(res + radd) to res_out when it is given.
+//   YM == kYSwiglu: rows interleaved gate/up in blocks of 8; Y[8g + j] = silu(g) * u.
+enum { kXPlain = 0, kXNorm = 1, kXNormAdd = 2 };
+enum { kYPlain = 0, kYSwiglu = 1 };
+constexpr int kXVecs = 4;  // 16-byte activation vectors per thread loaded ahead of the weights
+struct M1Fuse {
+  const uint16_t* res = nullptr;
+  const uint16_t* radd = nullptr;
+  const uint16_t* nw = nullptr;
+  uint16_t* res_out = nullptr;
+  float eps = 0.f;
+};
+// Decode GEMV with fusions; the plan must be an M = 1 plan (p.m1). -2 if the shape does not
+// fit the fused kernel (checked on the host before any launch).
+hipError_t launch_gemv_fused(const GemvArgs& a, const GemvPlan& p, const M1Fuse& fz, bool norm,
+                             bool swiglu, hipStream_t st, int* reject);
+
 struct GemmArgs {
   const uint16_t* A;   // X [M][K] bf16
   const uint32_t* Wq;  // [N][K/8]

@@ -26,9 +26,13 @@ SIGNATURES = {
     "ns_rope": [_VP, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I64, _I64, _VP],
     "ns_swiglu": [_VP, _VP, _VP, _I32, _I32, _VP],
     "ns_decode_qkv": [_VP, _VP, _VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP],
-    "ns_decode_attention_workspace": [_I32, _I32, _I32],
+    "ns_decode_attention_workspace": [_I32, _I32, _I32, _I32],
     "ns_decode_attention": [_VP, _VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32, _I32, _VP],
+    "ns_decode_qkv_attention": [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32,
+                                _I32, _VP],
 }
+SIGNATURES["ns_w4_gemv_decode"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _I32, _I32, _I32,
+                                   _I32, _VP]
 RESTYPES = {"ns_decode_attention_workspace": _SZ}
 
 
@@ -189,16 +193,20 @@ class Kernels:
                                     k_cache.shape[-2], self._stream())
         self._check(rc, "ns_decode_qkv")
 
-    def decode_attention_workspace(self, n_heads, head_dim, max_len):
-        """Bytes of device workspace decode_attention needs."""
-        return int(self.lib.ns_decode_attention_workspace(n_heads, head_dim, max_len))
+    def decode_attention_workspace(self, n_heads, n_kv_heads, head_dim, max_len, device=None):
+        """A uint8 device tensor of the workspace decode_attention and decode_qkv_attention
+        need (per-split partial results). Launches that may overlap in time need workspaces of
+        their own."""
+        n = int(self.lib.ns_decode_attention_workspace(n_heads, n_kv_heads, head_dim, max_len))
+        if n == 0:
+            raise ValueError("unsupported attention sizes (head_dim must be 128)")
+        return torch.zeros(n, dtype=torch.uint8, device=device or "cuda")
 
     def decode_attention(self, q, k_cache, v_cache, pos, n_heads, n_kv_heads, head_dim,
                          work, out=None):
         """Attention of one query token q [Hq * D] over cache rows 0 .. pos[0] of one layer's
         k_cache / v_cache [Hk, max_len, D]; returns out [1, Hq * D] bf16. The reference uses
-        PyTorch SDPA for this (qwen.py:124-133). work: a uint8 device tensor of at least
-        decode_attention_workspace(...) bytes."""
+        PyTorch SDPA for this (qwen.py:124-133). work: from decode_attention_workspace."""
         _require_gpu_tensor(q, "q", torch.bfloat16)
         _require_gpu_tensor(pos, "pos", torch.int32)
         _require_gpu_tensor(work, "work", torch.uint8)
@@ -209,4 +217,63 @@ class Kernels:
                                           work.numel(), n_heads, n_kv_heads, head_dim,
                                           k_cache.shape[-2], self._stream())
         self._check(rc, "ns_decode_attention")
+        return out
+
+    def decode_qkv_attention(self, qkv, bias, inv_freq, pos, k_cache, v_cache, n_heads,
+                             n_kv_heads, head_dim, work, out=None):
+        """decode_qkv followed by decode_attention in one launch, qkv left unchanged: bias +
+        RoPE of the q heads, the token's k / v row appended to the cache at pos[0], attention
+        over rows 0 .. pos[0]. Returns out [1, Hq * D] bf16."""
+        _require_gpu_tensor(qkv, "qkv", torch.bfloat16)
+        _require_gpu_tensor(inv_freq, "inv_freq", torch.float32)
+        _require_gpu_tensor(pos, "pos", torch.int32)
+        _require_gpu_tensor(work, "work", torch.uint8)
+        for t, n in ((k_cache, "k_cache"), (v_cache, "v_cache")):
+            _require_gpu_tensor(t, n, torch.bfloat16)
+            if not t.is_contiguous():
+                raise ValueError(f"{n} must be contiguous")
+        if bias is not None:
+            _require_gpu_tensor(bias, "bias", torch.bfloat16)
+        if not qkv.is_contiguous():
+            raise ValueError("qkv must be contiguous")
+        if out is None:
+            out = torch.empty((1, n_heads * head_dim), dtype=torch.bfloat16, device=qkv.device)
+        rc = self.lib.ns_decode_qkv_attention(
+            qkv.data_ptr(), None if bias is None else bias.data_ptr(), inv_freq.data_ptr(),
+            pos.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
+            work.data_ptr(), work.numel(), n_heads, n_kv_heads, head_dim, k_cache.shape[-2],
+            self._stream())
+        self._check(rc, "ns_decode_qkv_attention")
+        return out
+
+    def gemv_decode(self, Wq, S, group=128, x=None, res=None, r=None, norm_w=None, eps=1e-6,
+                    res_out=None, swiglu=False, out=None):
+        """One-token W4 GEMV with its neighbours fused (no reference counterpart; its runner
+        launches them separately, qwen.py:145-162). Activation: x [K] / [1, K], or, with res,
+        rmsnorm(res + r) * norm_w (res_out receives bf16(res + r)). Output: y [1, N], or with
+        ``swiglu`` (gate/up rows interleaved in blocks of 8) silu(gate) * up [1, N/2]."""
+        for t, n in ((Wq, "Wq"), (S, "S")):
+            _require_gpu_tensor(t, n, torch.int32 if n == "Wq" else torch.bfloat16)
+            if not t.is_contiguous():
+                raise ValueError(f"{n} must be contiguous")
+        N, K = Wq.shape[0], Wq.shape[1] * 8
+        vecs = {"x": x, "res": res, "r": r, "norm_w": norm_w, "res_out": res_out}
+        for n, t in vecs.items():
+            if t is not None:
+                _require_gpu_tensor(t, n, torch.bfloat16)
+                if t.numel() != K or not t.is_contiguous():
+                    raise ValueError(f"{n} must be a contiguous tensor of {K} elements")
+        n_out = N // 2 if swiglu else N
+        if out is None:
+            out = torch.empty((1, n_out), dtype=torch.bfloat16, device=Wq.device)
+        elif out.numel() != n_out or not out.is_contiguous() or out.dtype != torch.bfloat16:
+            raise ValueError(f"out must be a contiguous bf16 tensor of {n_out} elements")
+
+        def ptr(t):
+            return None if t is None else t.data_ptr()
+
+        rc = self.lib.ns_w4_gemv_decode(ptr(x), ptr(res), ptr(r), ptr(norm_w), eps, ptr(res_out),
+                                        Wq.data_ptr(), S.data_ptr(), out.data_ptr(), N, K, group,
+                                        1 if swiglu else 0, self._stream())
+        self._check(rc, "ns_w4_gemv_decode")
         return out

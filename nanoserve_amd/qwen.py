@@ -16,9 +16,11 @@ the same codes and scales as quantizing them one by one), and a one-token decode
 on device-resident token id and position (``decode``), so the whole step is captured once as
 a HIP graph and replayed for every token (``capture_decode``).
 
-Kernels used per decode step and layer: ns_w4_linear x4, ns_decode_qkv (bias + RoPE + KV
-append), ns_decode_attention (grouped-query attention over the cache), ns_rmsnorm x2,
-ns_swiglu. The prompt pass (T > 1) uses ns_w4_linear (GEMM for T > 8), ns_rope, ns_rmsnorm,
+Kernels used per decode step and layer: ns_w4_gemv_decode x4 (the q/k/v and gate/up GEMVs
+with the residual add + RMSNorm fused into their activation load, SwiGLU fused into the
+gate/up GEMV's output), ns_decode_qkv_attention (bias + RoPE + KV append + grouped-query
+attention over the cache). The gate/up weight rows are stored interleaved in blocks of 8
+(``interleave_gate_up``) so that a gate row and its up row land in the same 16-row group. The prompt pass (T > 1) uses ns_w4_linear (GEMM for T > 8), ns_rope, ns_rmsnorm,
 ns_swiglu, and fp32 PyTorch attention for the prompt's causal attention.
 
 No weights are downloaded: ``random`` builds a model of any Qwen2 shape with seeded random
@@ -71,6 +73,21 @@ class Qwen2Shape:
         return self.layers * self.w4_bytes_per_layer() + self.vocab * self.hidden * 2 + kv
 
 
+def interleave_gate_up(Wq: torch.Tensor, S: torch.Tensor):
+    """Row order of the fused gate/up projection used by the decode GEMV's SwiGLU output: rows
+    16b .. 16b+7 are gate rows 8b .. 8b+7 and rows 16b+8 .. 16b+15 the up rows 8b .. 8b+7
+    (gate rows 0 .. I-1 then up rows I .. 2I-1 on input). Rows are whole quantized rows, so
+    codes and scales move together and nothing is re-quantized."""
+    N = Wq.shape[0]
+    if N % 16:
+        raise ValueError("gate/up interleave needs the intermediate size to be a multiple of 8")
+
+    def perm(t):
+        return t.view(2, N // 16, 8, t.shape[1]).transpose(0, 1).reshape(N, t.shape[1]).contiguous()
+
+    return perm(Wq), perm(S)
+
+
 class Qwen2Runner:
     """W4A16 Qwen2 runner. Build with ``random`` or ``from_hf``; ``forward`` / ``generate`` have
     the reference's signatures and semantics (qwen.py:137-177)."""
@@ -97,11 +114,12 @@ class Qwen2Runner:
         self.tok = torch.zeros(1, dtype=torch.int64, device=self.dev)
         self.pos = torch.zeros(1, dtype=torch.int32, device=self.dev)
         self.x = torch.empty(1, H, **bf)
+        self.x2 = torch.empty(1, H, **bf)
         self.h = torch.empty(1, H, **bf)
         self.o = torch.empty(1, H, **bf)
+        self.d = torch.empty(1, H, **bf)
         self.qkv = torch.empty(1, shape.qkv_rows, **bf)
         self.attn = torch.empty(1, shape.heads * D, **bf)
-        self.gu = torch.empty(1, 2 * I, **bf)
         self.act = torch.empty(1, I, **bf)
         self.logits = torch.empty(1, shape.vocab, **bf)
         self.work = None
@@ -133,6 +151,7 @@ class Qwen2Runner:
                 W = randn(n, kk)
                 L[name] = k.w4_quantize(W, shape.group)
                 del W
+            L["wgu"] = interleave_gate_up(*L["wgu"])
             layers.append(L)
         embed = randn(shape.vocab, H)
         lm_head = randn(shape.vocab, H)
@@ -180,6 +199,7 @@ class Qwen2Runner:
                       "wd": [mlp.down_proj.weight]}
             for name, ws in stacks.items():
                 L[name] = k.w4_quantize(bf(torch.cat([w.detach() for w in ws])), group)
+            L["wgu"] = interleave_gate_up(*L["wgu"])
             layers.append(L)
         return cls(shape, bf(m.embed_tokens.weight), bf(m.norm.weight),
                    bf(hf_model.lm_head.weight), layers, k)
@@ -193,10 +213,8 @@ class Qwen2Runner:
         self.cache_k = torch.empty(shape, dtype=torch.bfloat16, device=self.dev)
         self.cache_v = torch.empty_like(self.cache_k)
         self.max_len = max_len
-        nbytes = self.k.decode_attention_workspace(s.heads, s.head_dim, max_len)
-        if nbytes == 0:
-            raise ValueError("decode attention supports head_dim 128 only")
-        self.work = torch.empty(nbytes, dtype=torch.uint8, device=self.dev)
+        self.work = self.k.decode_attention_workspace(s.heads, s.kv_heads, s.head_dim, max_len,
+                                                      device=self.dev)
         self.graph = None
 
     def _store_kv(self, li, k, v, pos0):
@@ -208,25 +226,35 @@ class Qwen2Runner:
     # ------------------------------------------------------------------ one-token decode step
     def _decode_body(self):
         """One decode step on self.tok / self.pos (device tensors) into self.logits. Launches
-        only; no allocation, no host synchronisation, so it can be captured."""
+        only; no allocation, no host synchronisation, so it can be captured.
+
+        Per layer five kernels: the q/k/v GEMV with the residual add + input RMSNorm fused
+        into its activation load, the attention (bias + RoPE + KV append + attention), the o
+        GEMV, the gate/up GEMV with the post-attention add + RMSNorm fused in and SwiGLU
+        fused into its output, and the down GEMV. The residual stream alternates between two
+        buffers (a fused GEMV reads one and one of its workgroups writes the other)."""
         s, k = self.shape, self.k
-        H, I, D, G = s.hidden, s.intermediate, s.head_dim, s.group
+        D, G, eps = s.head_dim, s.group, s.eps
         torch.index_select(self.embed, 0, self.tok, out=self.x)
-        k.rmsnorm(self.x, None, self.layers[0]["ln_in"], s.eps, out=self.h)
-        q = self.qkv[0, :s.heads * D]
+        resid, spare = self.x, self.x2
+        pending = None  # the addend not yet in the residual stream (the last down output)
         for li, L in enumerate(self.layers):
-            k.w4_linear(self.h, *L["wqkv"], G, out=self.qkv)
-            k.decode_qkv(self.qkv[0], L["bqkv"], self.inv_freq, self.pos, self.cache_k[li],
-                         self.cache_v[li], s.heads, s.kv_heads, D)
-            k.decode_attention(q, self.cache_k[li], self.cache_v[li], self.pos, s.heads,
-                               s.kv_heads, D, self.work, out=self.attn)
-            k.w4_linear(self.attn, *L["wo"], G, out=self.o)
-            k.rmsnorm(self.x, self.o, L["ln_post"], s.eps, out=self.h)
-            k.w4_linear(self.h, *L["wgu"], G, out=self.gu)
-            k.swiglu(self.gu[:, :I], self.gu[:, I:], out=self.act)
-            k.w4_linear(self.act, *L["wd"], G, out=self.o)
-            nxt = self.layers[li + 1]["ln_in"] if li + 1 < len(self.layers) else self.final_norm
-            k.rmsnorm(self.x, self.o, nxt, s.eps, out=self.h)
+            if pending is None:
+                k.gemv_decode(*L["wqkv"], G, res=resid, norm_w=L["ln_in"], eps=eps, out=self.qkv)
+            else:
+                k.gemv_decode(*L["wqkv"], G, res=resid, r=pending, norm_w=L["ln_in"], eps=eps,
+                              res_out=spare, out=self.qkv)
+                resid, spare = spare, resid
+            k.decode_qkv_attention(self.qkv[0], L["bqkv"], self.inv_freq, self.pos,
+                                   self.cache_k[li], self.cache_v[li], s.heads, s.kv_heads, D,
+                                   self.work, out=self.attn)
+            k.gemv_decode(*L["wo"], G, x=self.attn, out=self.o)
+            k.gemv_decode(*L["wgu"], G, res=resid, r=self.o, norm_w=L["ln_post"], eps=eps,
+                          res_out=spare, swiglu=True, out=self.act)
+            resid, spare = spare, resid
+            k.gemv_decode(*L["wd"], G, x=self.act, out=self.d)
+            pending = self.d
+        k.rmsnorm(resid, pending, self.final_norm, eps, out=self.h)
         torch.mm(self.h, self.lm_head.t(), out=self.logits)
 
     def _set_step(self, token, pos: int):
@@ -320,8 +348,8 @@ class Qwen2Runner:
                 self._store_kv(li, kk, v, pos0)
             a = self._prompt_attention(q, kk, v, pos0, li)
             h = k.rmsnorm(x, k.w4_linear(a, *L["wo"], G), L["ln_post"], s.eps)
-            gu = k.w4_linear(h, *L["wgu"], G)
-            act = k.swiglu(gu[:, :I].contiguous(), gu[:, I:].contiguous())
+            gu = k.w4_linear(h, *L["wgu"], G).view(T, I // 8, 2, 8)  # gate/up interleaved by 8
+            act = k.swiglu(gu[:, :, 0].reshape(T, I), gu[:, :, 1].reshape(T, I))
             nxt = self.layers[li + 1]["ln_in"] if li + 1 < len(self.layers) else self.final_norm
             h = k.rmsnorm(x, k.w4_linear(act, *L["wd"], G), nxt, s.eps)
         if last_only:

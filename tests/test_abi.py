@@ -34,7 +34,8 @@ def test_header_declares_the_reference_entry_points():
     # decode-step attention operators the reference does with PyTorch ops
     assert declared_symbols() == sorted([
         "ns_w4_linear", "ns_w4_quantize", "ns_rmsnorm", "ns_rope", "ns_swiglu",
-        "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention"])
+        "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention",
+        "ns_decode_qkv_attention", "ns_w4_gemv_decode"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -145,10 +146,11 @@ def test_decode_qkv_rejects_bad_arguments(k):
 
 
 def test_decode_attention_workspace_and_rejects(k):
-    ws = k.lib.ns_decode_attention_workspace(28, 128, 1024)
+    ws = k.lib.ns_decode_attention_workspace(28, 4, 128, 1024)
     assert ws == 16 * 28 * 130 * 4  # 64-row splits x heads x (D + max + sum) floats
-    assert k.lib.ns_decode_attention_workspace(28, 64, 1024) == 0
-    assert k.lib.ns_decode_attention_workspace(28, 128, 0) == 0
+    assert k.lib.ns_decode_attention_workspace(28, 4, 64, 1024) == 0
+    assert k.lib.ns_decode_attention_workspace(28, 4, 128, 0) == 0
+    assert k.lib.ns_decode_attention_workspace(28, 0, 128, 64) == 0
 
     def call(work_bytes=ws, Hq=28, Hk=4, D=128, L=1024, q=P, work=P):
         return k.lib.ns_decode_attention(q, P, P, P, P, work, work_bytes, Hq, Hk, D, L, None)
@@ -160,3 +162,30 @@ def test_decode_attention_workspace_and_rejects(k):
     assert call(L=0) == -2
     assert call(q=None) == -2
     assert call(work=P + 4) == -2
+
+    def fused(work_bytes=ws, Hq=28, Hk=4, D=128, L=1024, qkv=P, work=P):
+        return k.lib.ns_decode_qkv_attention(qkv, None, P, P, P, P, P, work, work_bytes, Hq, Hk,
+                                             D, L, None)
+
+    assert fused(work_bytes=ws - 1) == -2
+    assert fused(D=64) == -2
+    assert fused(Hq=36) == -2
+    assert fused(qkv=None) == -2
+    assert fused(qkv=P + 8) == -2
+    assert fused(work=None) == -2
+
+
+def test_gemv_decode_rejects_bad_arguments(k):
+    def call(X=P, res=None, r=None, nw=None, res_out=None, N=64, K=256, G=128, swiglu=0):
+        return k.lib.ns_w4_gemv_decode(X, res, r, nw, 1e-6, res_out, P, P, P, N, K, G, swiglu,
+                                       None)
+
+    assert call(G=64) == -2
+    assert call(K=192) == -2                       # K % 128
+    assert call(N=0) == -2
+    assert call(X=None) == -2                      # no activation
+    assert call(res=P) == -2                       # norm without weight
+    assert call(res=P, nw=P, K=16512) == -2        # norm row longer than 16384
+    assert call(N=40, swiglu=1) == -2              # SwiGLU pairs need N % 16 == 0
+    assert call(X=P + 8) == -2
+    assert call(res=P, nw=P, r=P + 0x1000, res_out=P) == -2  # res_out aliases res

@@ -130,8 +130,7 @@ def test_decode_attention(k, Hq, Hk, max_len, n):
     D = 128
     q = rnd(Hq * D, seed=11)
     kc, vc = rnd(Hk, max_len, D, seed=12), rnd(Hk, max_len, D, seed=13)
-    work = torch.empty(k.decode_attention_workspace(Hq, D, max_len), dtype=torch.uint8,
-                       device=DEV)
+    work = k.decode_attention_workspace(Hq, Hk, D, max_len)
     p = torch.tensor([n - 1], dtype=torch.int32, device=DEV)
     out = k.decode_attention(q, kc, vc, p, Hq, Hk, D, work)
     torch.cuda.synchronize()
@@ -142,8 +141,7 @@ def test_decode_attention_peaked_and_empty(k):
     Hq, Hk, D, max_len = 28, 4, 128, 300
     q = rnd(Hq * D, seed=14, scale=8.0)  # large logits: a few rows dominate each softmax
     kc, vc = rnd(Hk, max_len, D, seed=15), rnd(Hk, max_len, D, seed=16)
-    work = torch.empty(k.decode_attention_workspace(Hq, D, max_len), dtype=torch.uint8,
-                       device=DEV)
+    work = k.decode_attention_workspace(Hq, Hk, D, max_len)
     p = torch.tensor([250], dtype=torch.int32, device=DEV)
     out = k.decode_attention(q, kc, vc, p, Hq, Hk, D, work)
     torch.cuda.synchronize()
@@ -152,6 +150,145 @@ def test_decode_attention_peaked_and_empty(k):
     out = k.decode_attention(q, kc, vc, p, Hq, Hk, D, work)
     torch.cuda.synchronize()
     assert not out.any()
+
+
+# ------------------------------------------------------------------ ns_decode_qkv_attention
+@pytest.mark.parametrize("Hq,Hk", [(28, 4), (7, 1), (16, 4)])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_decode_qkv_attention(k, Hq, Hk, with_bias):
+    """The fused launch against the oracle's bias + RoPE followed by attention over the cache
+    with the new row appended, at positions inside, at the end of and across 64-row splits, at
+    the cache's last row, beyond it (no append, attention over the whole cache) and before row
+    0 (zeros); one workspace serves every launch in turn."""
+    D, max_len = 128, 300
+    qn, kn = Hq * D, Hk * D
+    work = k.decode_attention_workspace(Hq, Hk, D, max_len)
+    freq = R.inv_freq(D, 1000000.0)
+    kc, vc = rnd(Hk, max_len, D, seed=20), rnd(Hk, max_len, D, seed=21)
+    for i, pos in enumerate([0, 1, 63, 64, 65, 130, 299, 300, 450, -1]):
+        print(f"decode_qkv_attention Hq={Hq} Hk={Hk} bias={with_bias} pos={pos}", flush=True)
+        # moderate q so that the oracle's and the kernel's q roundings, which may differ by one
+        # bf16 ulp in rare elements, move the output by well under the tolerance
+        qkv = rnd(qn + 2 * kn, seed=30 + i, scale=0.5)
+        bias = rnd(qn + 2 * kn, seed=60 + i, scale=0.25) if with_bias else None
+        qkv0, kc0, vc0 = qkv.clone(), kc.clone(), vc.clone()
+        p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+        out = k.decode_qkv_attention(qkv, bias, freq.to(DEV), p, kc, vc, Hq, Hk, D, work)
+        torch.cuda.synchronize()
+        assert torch.equal(qkv, qkv0)  # qkv is not modified
+        q_ref, k_ref, v_ref = R.decode_qkv(qkv0, bias, Hq, Hk, D, pos, freq)
+        kc_ref, vc_ref = kc0.double().cpu(), vc0.double().cpu()
+        if 0 <= pos < max_len:
+            kc_ref[:, pos] = k_ref.reshape(Hk, D)
+            vc_ref[:, pos] = v_ref.reshape(Hk, D)
+            # the appended rows within a bf16 ulp of the oracle's, all other rows untouched
+            close(kc[:, pos], kc_ref[:, pos], rtol=2 ** -7, atol=1e-4)
+            assert torch.equal(vc[:, pos].double().cpu(), vc_ref[:, pos])
+            kc_ref[:, pos] = kc[:, pos].double().cpu()  # attend over what the kernel stored
+        assert torch.equal(kc.double().cpu(), kc_ref) and torch.equal(vc.double().cpu(), vc_ref)
+        n = min(pos + 1, max_len)
+        if n <= 0:
+            assert not out.any()
+            continue
+        qr = q_ref.reshape(-1).to(torch.bfloat16)
+        close(out.reshape(-1), R.decode_attention(qr, kc_ref.to(torch.bfloat16),
+                                                  vc_ref.to(torch.bfloat16), n, Hq, Hk),
+              atol=2e-3)
+
+
+# ------------------------------------------------------------------ ns_w4_gemv_decode
+def _w4(N, K, seed):
+    """Quantized random weights (GPU), as the runner's: N(0, 0.02) bf16 through the quantizer."""
+    W = rnd(N, K, seed=seed, scale=0.02)
+    return Kernels().w4_quantize(W, 128)
+
+
+def _ref_linear(x_bf16, Wq, S):
+    """float64 x @ deq(Wq, S)^T through the oracle (x: bf16 [K])."""
+    xb = x_bf16.reshape(1, -1).cpu().view(torch.int16).numpy().view("uint16")
+    return torch.from_numpy(O.linear_f64(xb, Wq.cpu().numpy().view("uint32"),
+                                         S.cpu().view(torch.int16).numpy().view("uint16"), 128))
+
+
+@pytest.mark.parametrize("N,K", [(4608, 3584), (3584, 18944), (100, 256), (64, 128)])
+def test_gemv_decode_plain_equals_w4_linear(k, N, K):
+    print(f"gemv_decode plain N={N} K={K}", flush=True)
+    Wq, S = _w4(N, K, seed=40)
+    x = rnd(1, K, seed=41)
+    y = k.gemv_decode(Wq, S, 128, x=x)
+    torch.cuda.synchronize()
+    assert torch.equal(y, k.w4_linear(x, Wq, S, 128))
+
+
+@pytest.mark.parametrize("N,K", [(4608, 3584), (37888, 3584), (256, 1024), (48, 8192)])
+@pytest.mark.parametrize("with_r", [True, False])
+def test_gemv_decode_rmsnorm_input(k, N, K, with_r):
+    """Activation rmsnorm(res + r) * w fused into the GEMV: the new residual stream bit-exact,
+    the output against the oracle's float64 product of the oracle-normalised activation."""
+    print(f"gemv_decode rmsnorm N={N} K={K} r={with_r}", flush=True)
+    Wq, S = _w4(N, K, seed=42)
+    res, r, w = rnd(K, seed=43, scale=3.0), rnd(K, seed=44), rnd(K, seed=45, scale=0.5)
+    res_out = torch.full((K,), 7.0, dtype=torch.bfloat16, device=DEV)
+    y = k.gemv_decode(Wq, S, 128, res=res, r=r if with_r else None, norm_w=w, eps=1e-6,
+                      res_out=res_out)
+    torch.cuda.synchronize()
+    v_ref, h_ref = R.rmsnorm(res.reshape(1, -1), r.reshape(1, -1) if with_r else None,
+                             w, 1e-6)
+    if with_r:
+        assert torch.equal(res_out.double().cpu(), v_ref.reshape(-1))
+    else:
+        assert (res_out == 7.0).all()  # nothing added: the residual stream is not rewritten
+    ref = _ref_linear(R.bf16_round(h_ref).to(torch.bfloat16), Wq, S)
+    # the activation is bf16-rounded from fp32 arithmetic: an element may land one ulp from
+    # the oracle's rounding, so the bound is the north-star one
+    err = (y.double().cpu() - ref).abs().max().item()
+    assert err <= 1e-2 * ref.abs().max().item(), err
+    # and against the unfused pair (ns_rmsnorm, then ns_w4_linear)
+    res2 = res.clone().reshape(1, -1)
+    h = k.rmsnorm(res2, r.reshape(1, -1) if with_r else None, w, 1e-6)
+    y2 = k.w4_linear(h, Wq, S, 128)
+    torch.cuda.synchronize()
+    close(y.reshape(-1), y2.reshape(-1).double().cpu(), rtol=2 ** -7,
+          atol=1e-3 * y2.abs().max().item())
+
+
+@pytest.mark.parametrize("N,K", [(37888, 3584), (2048, 896), (32, 256)])
+@pytest.mark.parametrize("norm", [True, False])
+def test_gemv_decode_swiglu_output(k, N, K, norm):
+    """SwiGLU fused into the output of the interleaved gate/up GEMV equals ns_w4_linear of the
+    same weights followed by ns_swiglu of the de-interleaved halves."""
+    from nanoserve_amd.qwen import interleave_gate_up
+
+    print(f"gemv_decode swiglu N={N} K={K} norm={norm}", flush=True)
+    Wq, S = interleave_gate_up(*_w4(N, K, seed=46))
+    x = rnd(1, K, seed=47)
+    w = rnd(K, seed=48, scale=0.5)
+    if norm:
+        act = k.gemv_decode(Wq, S, 128, res=x, norm_w=w, eps=1e-6, swiglu=True)
+        xin = k.rmsnorm(x.clone(), None, w, 1e-6)
+    else:
+        act = k.gemv_decode(Wq, S, 128, x=x, swiglu=True)
+        xin = x
+    gu = k.gemv_decode(Wq, S, 128, res=x, norm_w=w, eps=1e-6) if norm else k.w4_linear(
+        xin, Wq, S, 128)
+    I = N // 2
+    g4 = gu.view(I // 8, 2, 8)
+    ref = k.swiglu(g4[:, 0].reshape(1, I).contiguous(), g4[:, 1].reshape(1, I).contiguous())
+    torch.cuda.synchronize()
+    assert act.shape == (1, I)
+    close(act, ref.double().cpu(), rtol=2 ** -8, atol=1e-6)
+
+
+def test_gemv_decode_rejects(k):
+    Wq, S = _w4(64, 256, seed=49)
+    x = rnd(1, 256, seed=50)
+    with pytest.raises(RuntimeError):  # G != 128
+        k.gemv_decode(Wq, S, 64, x=x)
+    Wq2, S2 = _w4(40, 256, seed=51)
+    with pytest.raises(RuntimeError):  # N % 16 with swiglu
+        k.gemv_decode(Wq2, S2, 128, x=x, swiglu=True)
+    with pytest.raises(RuntimeError):  # res_out aliasing res
+        k.gemv_decode(Wq, S, 128, res=x, r=x, norm_w=x, res_out=x)
 
 
 # ------------------------------------------------------------------ the runner
@@ -187,9 +324,9 @@ def _effective_hf(m, runner):
             for b in (at.q_proj.bias, at.k_proj.bias, at.v_proj.bias):
                 b.copy_(r16(b))
             at.o_proj.weight.copy_(deq(L["wo"]))
-            wgu = deq(L["wgu"])
-            mlp.gate_proj.weight.copy_(wgu[:I])
-            mlp.up_proj.weight.copy_(wgu[I:])
+            wgu = deq(L["wgu"]).view(I // 8, 2, 8, -1)  # gate/up rows interleaved by 8
+            mlp.gate_proj.weight.copy_(wgu[:, 0].reshape(I, -1))
+            mlp.up_proj.weight.copy_(wgu[:, 1].reshape(I, -1))
             mlp.down_proj.weight.copy_(deq(L["wd"]))
             for ln in (layer.input_layernorm, layer.post_attention_layernorm):
                 ln.weight.copy_(r16(ln.weight))
