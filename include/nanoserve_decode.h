@@ -93,11 +93,13 @@ int ns_decode_attention(const void* q, const void* k_cache, const void* v_cache,
  * one launch, without modifying qkv: the q heads get bias + RoPE at position *pos, the new k
  * (bias + RoPE) and v (bias) rows are appended to the cache at row *pos, and out [Hq][D] is the
  * attention of the rotated q over rows 0 .. min(*pos + 1, max_len) - 1. Same arguments,
- * workspace and return codes as those two.
+ * workspace and return codes as those two. merge == 0 leaves the per-split partial results in
+ * the workspace instead of merging them (out is then written only when the rows fit one
+ * split): ns_w4_gemv_decode_attn merges them while it loads its activation.
  */
 int ns_decode_qkv_attention(const void* qkv, const void* bias, const void* inv_freq,
                             const int* pos, void* k_cache, void* v_cache, void* out, void* work,
-                            size_t work_bytes, int Hq, int Hk, int D, int max_len,
+                            size_t work_bytes, int Hq, int Hk, int D, int max_len, int merge,
                             void* stream);
 
 /*
@@ -120,6 +122,19 @@ int ns_decode_qkv_attention(const void* qkv, const void* bias, const void* inv_f
 int ns_w4_gemv_decode(const void* X, const void* res, const void* r, const void* norm_w,
                       float eps, void* res_out, const void* Wq, const void* S, void* Y, int N,
                       int K, int G, int swiglu, void* stream);
+
+/*
+ * No counterpart in the reference's C ABI: ns_w4_gemv_decode (plain activation, Y [N] =
+ * x . deq(Wq, S)^T) whose activation x [K = Hq * 128] is the output of an
+ * ns_decode_qkv_attention(..., merge = 0) launched before it on the same stream with the same
+ * pos, max_len, Hq and workspace: when that attention used more than one split of the cache
+ * rows, their partial results are merged here (fp32, as the attention's own merge); otherwise
+ * attn_out [K] bf16, which the attention then wrote, is read. Returns -2 for K != Hq * 128,
+ * G != 128, max_len <= 0, NULL or misaligned pointers.
+ */
+int ns_w4_gemv_decode_attn(const void* attn_out, const void* work, const int* pos, int max_len,
+                           int Hq, const void* Wq, const void* S, void* Y, int N, int K, int G,
+                           void* stream);
 
 #ifdef __cplusplus
 }

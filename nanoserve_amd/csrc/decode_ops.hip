@@ -210,12 +210,15 @@ __global__ void __launch_bounds__(kBlock)
 // per-head max and sum need two lane swaps instead of a 64-lane reduction per head; the values
 // are a VALU loop, each lane two dims of each of the wave's rows (one 4-byte load per row: the
 // wave reads each 256-byte row whole), probabilities broadcast from LDS.
-constexpr int kChunk = 64;
+constexpr int kAttnWaves = 16;             // waves per attention workgroup, 16 rows each
+constexpr int kAttnBlock = kAttnWaves * kWave;
+constexpr int kChunk = kAttnDecodeChunk;   // cache rows per split
+static_assert(kChunk == 16 * kAttnWaves, "one 16-row score tile per wave");
 constexpr int kHeadDim = 128;
 constexpr int kMaxGroup = 8;  // query heads per kv head (score columns 0..7 of 16 used)
 
 template <bool kFused>
-__global__ void __launch_bounds__(kBlock)
+__global__ void __launch_bounds__(kAttnBlock)
     decode_attn_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ bias,
                        const float* __restrict__ inv_freq, uint16_t* __restrict__ kc,
                        uint16_t* __restrict__ vc, const int* __restrict__ pos_p,
@@ -223,7 +226,7 @@ __global__ void __launch_bounds__(kBlock)
                        float* __restrict__ ml, int Hq, int Hk, int max_len, float qscale) {
   constexpr int D = kHeadDim;
   constexpr int RP = kMaxGroup;
-  constexpr int NWV = kBlock / kWave;
+  constexpr int NWV = kAttnWaves;
   constexpr int QS = D + 8;  // padded q row (bf16 elements)
   __shared__ __attribute__((aligned(16))) uint16_t qb[16][QS];
   __shared__ __attribute__((aligned(16))) float ps[kChunk][RP];
@@ -241,7 +244,7 @@ __global__ void __launch_bounds__(kBlock)
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   if (n <= 0) {  // no rows: zeros (uniform over the workgroup)
     if (split == 0)
-      for (int i = tid; i < R * D; i += kBlock) out[(size_t)g * R * D + i] = 0;
+      for (int i = tid; i < R * D; i += kAttnBlock) out[(size_t)g * R * D + i] = 0;
     return;
   }
   const int start = split * kChunk;
@@ -400,7 +403,9 @@ __global__ void __launch_bounds__(kBlock)
   m = fmaxf(m, __shfl_xor(m, 32, kWave));
   if (grp == 0) red_m[w][h] = m;
   __syncthreads();
-  m = fmaxf(fmaxf(red_m[0][h], red_m[1][h]), fmaxf(red_m[2][h], red_m[3][h]));
+  m = red_m[0][h];
+#pragma unroll
+  for (int i = 1; i < NWV; ++i) m = fmaxf(m, red_m[i][h]);
   float l = 0.f;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -438,19 +443,27 @@ __global__ void __launch_bounds__(kBlock)
   __syncthreads();
 
   const bool single = nsplit == 1;
-  for (int i = tid; i < R * D; i += kBlock) {
+  for (int i = tid; i < R * D; i += kAttnBlock) {
     const int hh = i / D, d = i % D;
-    const float o = (ored[0][hh][d] + ored[1][hh][d]) + (ored[2][hh][d] + ored[3][hh][d]);
+    float o = 0.f;
+#pragma unroll
+    for (int k = 0; k < NWV; ++k) o += ored[k][hh][d];
     if (single) {
-      const float lt = (red_l[0][hh] + red_l[1][hh]) + (red_l[2][hh] + red_l[3][hh]);
+      float lt = 0.f;
+#pragma unroll
+      for (int k = 0; k < NWV; ++k) lt += red_l[k][hh];
       out[(size_t)(g * R + hh) * D + d] = static_cast<uint16_t>(f32_to_bf16_rne(o / lt));
     } else {
       opart[((size_t)split * Hq + g * R + hh) * D + d] = o;
     }
   }
   if (!single && tid < R) {
-    const float mt = fmaxf(fmaxf(red_m[0][tid], red_m[1][tid]), fmaxf(red_m[2][tid], red_m[3][tid]));
-    const float lt = (red_l[0][tid] + red_l[1][tid]) + (red_l[2][tid] + red_l[3][tid]);
+    float mt = red_m[0][tid], lt = 0.f;
+#pragma unroll
+    for (int k = 0; k < NWV; ++k) {
+      mt = fmaxf(mt, red_m[k][tid]);
+      lt += red_l[k][tid];
+    }
     *reinterpret_cast<float2*>(&ml[((size_t)split * Hq + g * R + tid) * 2]) = make_float2(mt, lt);
   }
 }
@@ -570,18 +583,18 @@ int attn_check(int Hq, int Hk, int D, int max_len, size_t work_bytes, const void
 template <bool kFused>
 int launch_attn(const void* q, const void* bias, const void* inv_freq, void* kc, void* vc,
                 const int* pos, void* out, void* work, int Hq, int Hk, int max_len,
-                hipStream_t st) {
+                hipStream_t st, bool merge = true) {
   const size_t splits = attn_splits(max_len);
   float* opart = static_cast<float*>(work);
   float* ml = opart + splits * Hq * kHeadDim;
   const float qscale = 1.4426950408889634f / sqrtf(static_cast<float>(kHeadDim));  // log2(e)/sqrt(D)
   const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(Hk));
-  hipLaunchKernelGGL(decode_attn_kernel<kFused>, grid, dim3(kBlock), 0, st,
+  hipLaunchKernelGGL(decode_attn_kernel<kFused>, grid, dim3(kAttnBlock), 0, st,
                      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(bias),
                      static_cast<const float*>(inv_freq), static_cast<uint16_t*>(kc),
                      static_cast<uint16_t*>(vc), pos, static_cast<uint16_t*>(out), opart, ml, Hq,
                      Hk, max_len, qscale);
-  if (splits > 1) {
+  if (merge && splits > 1) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
     hipLaunchKernelGGL(decode_attn_merge_kernel, dim3(Hk), dim3(kBlock), 0, st, opart, ml, pos,
@@ -679,7 +692,7 @@ int ns_decode_attention(const void* q, const void* k_cache, const void* v_cache,
 
 int ns_decode_qkv_attention(const void* qkv, const void* bias, const void* inv_freq,
                             const int* pos, void* k_cache, void* v_cache, void* out, void* work,
-                            size_t work_bytes, int Hq, int Hk, int D, int max_len,
+                            size_t work_bytes, int Hq, int Hk, int D, int max_len, int merge,
                             void* stream) {
   const int rc = ns::attn_check(Hq, Hk, D, max_len, work_bytes, work);
   if (rc) return rc;
@@ -689,7 +702,7 @@ int ns_decode_qkv_attention(const void* qkv, const void* bias, const void* inv_f
       !ns::aligned(out, 2))
     return -2;
   return ns::launch_attn<true>(qkv, bias, inv_freq, k_cache, v_cache, pos, out, work, Hq, Hk,
-                               max_len, static_cast<hipStream_t>(stream));
+                               max_len, static_cast<hipStream_t>(stream), merge != 0);
 }
 
 }  // extern "C"

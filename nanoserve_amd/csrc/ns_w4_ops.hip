@@ -7,6 +7,7 @@
 
 #include "../../include/nanoserve_decode.h"
 #include "../../include/nanoserve_w4.h"
+#include "w4_common.h"
 #include "w4_kernels.h"
 
 namespace {
@@ -78,6 +79,32 @@ int ns_w4_gemv_decode(const void* X, const void* res, const void* r, const void*
   const hipError_t e = ns::launch_gemv_fused(a, ns::gemv_plan(1, N, K, G), fz, res != nullptr,
                                              swiglu != 0, static_cast<hipStream_t>(stream),
                                              &reject);
+  if (reject) return -2;
+  if (e != hipSuccess) return static_cast<int>(e);
+  return last_status();
+}
+
+int ns_w4_gemv_decode_attn(const void* attn_out, const void* work, const int* pos, int max_len,
+                           int Hq, const void* Wq, const void* S, void* Y, int N, int K, int G,
+                           void* stream) {
+  if (N <= 0 || K <= 0 || G != 128 || Hq <= 0 || K != Hq * 128 || max_len <= 0) return -2;
+  if (!attn_out || !work || !pos || !Wq || !S || !Y) return -2;
+  if (!aligned(attn_out, 16) || !aligned(work, 16) || !aligned(pos, 4) || !aligned(Wq, 16) ||
+      !aligned(S, 2) || !aligned(Y, 2))
+    return -2;
+  const ns::GemvArgs a{static_cast<const uint16_t*>(attn_out), static_cast<const uint32_t*>(Wq),
+                       static_cast<const uint16_t*>(S), static_cast<uint16_t*>(Y), 1, N, K, G};
+  const size_t splits = (static_cast<size_t>(max_len) + ns::kAttnDecodeChunk - 1) /
+                        ns::kAttnDecodeChunk;
+  ns::M1Fuse fz;
+  fz.opart = static_cast<const float*>(work);
+  fz.ml = fz.opart + splits * static_cast<size_t>(K);
+  fz.pos = pos;
+  fz.max_len = max_len;
+  fz.heads = Hq;
+  int reject = 0;
+  const hipError_t e = ns::launch_gemv_attn(a, ns::gemv_plan(1, N, K, G), fz,
+                                            static_cast<hipStream_t>(stream), &reject);
   if (reject) return -2;
   if (e != hipSuccess) return static_cast<int>(e);
   return last_status();

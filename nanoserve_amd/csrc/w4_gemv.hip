@@ -463,10 +463,33 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, 16u * e, 0, 0));
   };
   u32x4_t xa[XV], xb[XV], xw[XV];
+  // attention merge: this thread's 8 dims (head e / 16) of the first kAttnBatch splits
+  constexpr int kAttnBatch = 4;
+  float2 aml[kAttnBatch];
+  f32x4_t ao[kAttnBatch][2];
+  int nsplit = 0;
   if constexpr (XM == kXPlain) {
     const auto rx = vec_rsrc(X);
 #pragma unroll
     for (int i = 0; i < XV; ++i) xa[i] = vec_load(rx, tid + i * NT);
+  } else if constexpr (XM == kXAttn) {
+    static_assert(XV == 1, "one activation vector per thread");
+    const int n = min(*fz.pos + 1, fz.max_len);
+    nsplit = n > 0 ? (n + kAttnDecodeChunk - 1) / kAttnDecodeChunk : 0;
+    xa[0] = vec_load(vec_rsrc(X), tid);
+    const int hq = tid >> 4, d0 = 8 * (tid & 15);
+#pragma unroll
+    for (int sp = 0; sp < kAttnBatch; ++sp) {
+      aml[sp] = make_float2(-INFINITY, 0.f);
+      ao[sp][0] = ao[sp][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if (nsplit > 1 && sp < nsplit && tid < KV) {
+        aml[sp] = *reinterpret_cast<const float2*>(&fz.ml[((size_t)sp * fz.heads + hq) * 2]);
+        const f32x4_t* src = reinterpret_cast<const f32x4_t*>(
+            &fz.opart[((size_t)sp * fz.heads + hq) * 128 + d0]);
+        ao[sp][0] = src[0];
+        ao[sp][1] = src[1];
+      }
+    }
   } else {
     const auto rr = vec_rsrc(fz.res), rw = vec_rsrc(fz.nw);
 #pragma unroll
@@ -487,7 +510,51 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   for (int u = 0; u < R; ++u) issue(ring[u], rsc[u]);
   __builtin_amdgcn_sched_barrier(0);
 
-  if constexpr (XM != kXPlain) {
+  if constexpr (XM == kXAttn) {
+    // merge the splits as the attention's own merge does: rescale to the running max
+    // (base-2 logits), sum, divide once
+    u32x4_t xv = xa[0];
+    if (nsplit > 1) {
+      const int hq = tid >> 4, d0 = 8 * (tid & 15);
+      float m = -INFINITY, l = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int s0 = 0; s0 < nsplit; s0 += kAttnBatch) {
+        if (s0 > 0) {  // later batches (contexts beyond 4 splits)
+#pragma unroll
+          for (int sp = 0; sp < kAttnBatch; ++sp) {
+            aml[sp] = make_float2(-INFINITY, 0.f);
+            ao[sp][0] = ao[sp][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            if (s0 + sp < nsplit && tid < KV) {
+              const size_t row = (size_t)(s0 + sp) * fz.heads + hq;
+              aml[sp] = *reinterpret_cast<const float2*>(&fz.ml[row * 2]);
+              const f32x4_t* src = reinterpret_cast<const f32x4_t*>(&fz.opart[row * 128 + d0]);
+              ao[sp][0] = src[0];
+              ao[sp][1] = src[1];
+            }
+          }
+        }
+#pragma unroll
+        for (int sp = 0; sp < kAttnBatch; ++sp) {
+          const float mn = fmaxf(m, aml[sp].x);
+          if (mn == -INFINITY) continue;  // nothing yet (absent splits)
+          const float fo = exp2f(m - mn), fs = exp2f(aml[sp].x - mn);
+          l = l * fo + aml[sp].y * fs;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[q] = acc[q] * fo + ao[sp][0][q] * fs;
+            acc[4 + q] = acc[4 + q] * fo + ao[sp][1][q] * fs;
+          }
+          m = mn;
+        }
+      }
+      const float il = 1.f / l;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[q] *= il;
+      xv = pack8(acc);
+    }
+    if (tid < 16 * CP)
+      *reinterpret_cast<u32x4_t*>(&xl[(tid >> 4) * XR + 8 * (tid & 15)]) =
+          tid < KV ? pair_order(xv) : u32x4_t{0u, 0u, 0u, 0u};
+  } else if constexpr (XM != kXPlain) {
     // x = rmsnorm(res + radd) * nw, as the fused RMSNorm kernel: residual rounded to bf16,
     // sum of squares over the row (wave sums, then the workgroup's in LDS), one bf16 rounding
     // of v * inv * w; one workgroup also stores the new residual stream.
@@ -1051,6 +1118,22 @@ hipError_t launch_m1_fused(const GemvArgs& a, const M1Fuse& fz, bool norm, bool 
 }
 
 }  // namespace
+
+hipError_t launch_gemv_attn(const GemvArgs& a, const GemvPlan& p, const M1Fuse& fz,
+                            hipStream_t st, int* reject) {
+  *reject = 0;
+  const int C = a.K >> 7, CP = (C + 15) & ~15;
+  if (!p.m1 || p.rt != 2 || 16 * CP > p.nw * kWave) {
+    *reject = 1;
+    return hipSuccess;
+  }
+  if (p.nw == 16 && p.gr == 16) return launch_m1<16, 2, 16, kXAttn, kYPlain, 1>(a, st, fz);
+  if (p.nw == 14 && p.gr == 16) return launch_m1<14, 2, 16, kXAttn, kYPlain, 1>(a, st, fz);
+  if (p.nw == 8 && p.gr == 16) return launch_m1<8, 2, 16, kXAttn, kYPlain, 1>(a, st, fz);
+  if (p.nw == 8 && p.gr == 8) return launch_m1<8, 2, 8, kXAttn, kYPlain, 1>(a, st, fz);
+  *reject = 1;
+  return hipSuccess;
+}
 
 hipError_t launch_gemv_fused(const GemvArgs& a, const GemvPlan& p, const M1Fuse& fz, bool norm,
                              bool swiglu, hipStream_t st, int* reject) {

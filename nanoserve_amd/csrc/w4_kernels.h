@@ -33,7 +33,10 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st);
 //   XM == kXNormAdd: the activation is rmsnorm(res + radd) * nw; workgroup 0 stores
 //                    bf16(res + radd) to res_out when it is given.
 //   YM == kYSwiglu: rows interleaved gate/up in blocks of 8; Y[8g + j] = silu(g) * u.
-enum { kXPlain = 0, kXNorm = 1, kXNormAdd = 2 };
+//   XM == kXAttn:    the activation is the decode attention's output: the merge of its
+//                    per-split partials (opart [splits][heads][128], ml [splits][heads][2])
+//                    when it used more than one split, else X (bf16, written by it).
+enum { kXPlain = 0, kXNorm = 1, kXNormAdd = 2, kXAttn = 3 };
 enum { kYPlain = 0, kYSwiglu = 1 };
 constexpr int kXVecs = 4;  // 16-byte activation vectors per thread loaded ahead of the weights
 struct M1Fuse {
@@ -42,7 +45,14 @@ struct M1Fuse {
   const uint16_t* nw = nullptr;
   uint16_t* res_out = nullptr;
   float eps = 0.f;
+  const float* opart = nullptr;
+  const float* ml = nullptr;
+  const int* pos = nullptr;
+  int max_len = 0;
+  int heads = 0;
 };
+hipError_t launch_gemv_attn(const GemvArgs& a, const GemvPlan& p, const M1Fuse& fz,
+                            hipStream_t st, int* reject);
 // Decode GEMV with fusions; the plan must be an M = 1 plan (p.m1). -2 if the shape does not
 // fit the fused kernel (checked on the host before any launch).
 hipError_t launch_gemv_fused(const GemvArgs& a, const GemvPlan& p, const M1Fuse& fz, bool norm,

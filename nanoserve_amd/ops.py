@@ -29,7 +29,8 @@ SIGNATURES = {
     "ns_decode_attention_workspace": [_I32, _I32, _I32, _I32],
     "ns_decode_attention": [_VP, _VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32, _I32, _VP],
     "ns_decode_qkv_attention": [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32,
-                                _I32, _VP],
+                                _I32, _I32, _VP],
+    "ns_w4_gemv_decode_attn": [_VP, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _I32, _I32, _I32, _VP],
 }
 SIGNATURES["ns_w4_gemv_decode"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _I32, _I32, _I32,
                                    _I32, _VP]
@@ -220,10 +221,11 @@ class Kernels:
         return out
 
     def decode_qkv_attention(self, qkv, bias, inv_freq, pos, k_cache, v_cache, n_heads,
-                             n_kv_heads, head_dim, work, out=None):
+                             n_kv_heads, head_dim, work, out=None, merge=True):
         """decode_qkv followed by decode_attention in one launch, qkv left unchanged: bias +
         RoPE of the q heads, the token's k / v row appended to the cache at pos[0], attention
-        over rows 0 .. pos[0]. Returns out [1, Hq * D] bf16."""
+        over rows 0 .. pos[0]. Returns out [1, Hq * D] bf16. With ``merge=False`` the split
+        partials stay in ``work`` for gemv_decode_attn (out is written only for one split)."""
         _require_gpu_tensor(qkv, "qkv", torch.bfloat16)
         _require_gpu_tensor(inv_freq, "inv_freq", torch.float32)
         _require_gpu_tensor(pos, "pos", torch.int32)
@@ -242,8 +244,28 @@ class Kernels:
             qkv.data_ptr(), None if bias is None else bias.data_ptr(), inv_freq.data_ptr(),
             pos.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
             work.data_ptr(), work.numel(), n_heads, n_kv_heads, head_dim, k_cache.shape[-2],
-            self._stream())
+            1 if merge else 0, self._stream())
         self._check(rc, "ns_decode_qkv_attention")
+        return out
+
+    def gemv_decode_attn(self, attn_out, work, pos, max_len, n_heads, Wq, S, group=128,
+                         out=None):
+        """y [1, N] = a . deq(Wq, S)^T where a is the output of a preceding
+        decode_qkv_attention(..., merge=False) with the same work, pos, max_len and heads: its
+        split partials are merged while the activation is loaded."""
+        _require_gpu_tensor(attn_out, "attn_out", torch.bfloat16)
+        _require_gpu_tensor(work, "work", torch.uint8)
+        _require_gpu_tensor(pos, "pos", torch.int32)
+        _require_gpu_tensor(Wq, "Wq", torch.int32)
+        _require_gpu_tensor(S, "S", torch.bfloat16)
+        N, K = Wq.shape[0], Wq.shape[1] * 8
+        if out is None:
+            out = torch.empty((1, N), dtype=torch.bfloat16, device=Wq.device)
+        rc = self.lib.ns_w4_gemv_decode_attn(attn_out.data_ptr(), work.data_ptr(),
+                                             pos.data_ptr(), max_len, n_heads, Wq.data_ptr(),
+                                             S.data_ptr(), out.data_ptr(), N, K, group,
+                                             self._stream())
+        self._check(rc, "ns_w4_gemv_decode_attn")
         return out
 
     def gemv_decode(self, Wq, S, group=128, x=None, res=None, r=None, norm_w=None, eps=1e-6,

@@ -16,10 +16,11 @@ the same codes and scales as quantizing them one by one), and a one-token decode
 on device-resident token id and position (``decode``), so the whole step is captured once as
 a HIP graph and replayed for every token (``capture_decode``).
 
-Kernels used per decode step and layer: ns_w4_gemv_decode x4 (the q/k/v and gate/up GEMVs
+Kernels used per decode step and layer: ns_w4_gemv_decode x3 (the q/k/v and gate/up GEMVs
 with the residual add + RMSNorm fused into their activation load, SwiGLU fused into the
-gate/up GEMV's output), ns_decode_qkv_attention (bias + RoPE + KV append + grouped-query
-attention over the cache). The gate/up weight rows are stored interleaved in blocks of 8
+gate/up GEMV's output; the down GEMV), ns_decode_qkv_attention (bias + RoPE + KV append +
+grouped-query attention over the cache, splits left unmerged) and ns_w4_gemv_decode_attn
+(the o GEMV, merging the attention's splits while loading its activation). The gate/up weight rows are stored interleaved in blocks of 8
 (``interleave_gate_up``) so that a gate row and its up row land in the same 16-row group. The prompt pass (T > 1) uses ns_w4_linear (GEMM for T > 8), ns_rope, ns_rmsnorm,
 ns_swiglu, and fp32 PyTorch attention for the prompt's causal attention.
 
@@ -229,9 +230,10 @@ class Qwen2Runner:
         only; no allocation, no host synchronisation, so it can be captured.
 
         Per layer five kernels: the q/k/v GEMV with the residual add + input RMSNorm fused
-        into its activation load, the attention (bias + RoPE + KV append + attention), the o
-        GEMV, the gate/up GEMV with the post-attention add + RMSNorm fused in and SwiGLU
-        fused into its output, and the down GEMV. The residual stream alternates between two
+        into its activation load, the attention (bias + RoPE + KV append + attention over
+        256-row splits of the cache), the o GEMV, which merges the attention's splits as it
+        loads its activation, the gate/up GEMV with the post-attention add + RMSNorm fused in
+        and SwiGLU fused into its output, and the down GEMV. The residual stream alternates between two
         buffers (a fused GEMV reads one and one of its workgroups writes the other)."""
         s, k = self.shape, self.k
         D, G, eps = s.head_dim, s.group, s.eps
@@ -247,8 +249,9 @@ class Qwen2Runner:
                 resid, spare = spare, resid
             k.decode_qkv_attention(self.qkv[0], L["bqkv"], self.inv_freq, self.pos,
                                    self.cache_k[li], self.cache_v[li], s.heads, s.kv_heads, D,
-                                   self.work, out=self.attn)
-            k.gemv_decode(*L["wo"], G, x=self.attn, out=self.o)
+                                   self.work, out=self.attn, merge=False)
+            k.gemv_decode_attn(self.attn, self.work, self.pos, self.max_len, s.heads, *L["wo"],
+                               G, out=self.o)
             k.gemv_decode(*L["wgu"], G, res=resid, r=self.o, norm_w=L["ln_post"], eps=eps,
                           res_out=spare, swiglu=True, out=self.act)
             resid, spare = spare, resid

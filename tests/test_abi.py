@@ -35,7 +35,7 @@ def test_header_declares_the_reference_entry_points():
     assert declared_symbols() == sorted([
         "ns_w4_linear", "ns_w4_quantize", "ns_rmsnorm", "ns_rope", "ns_swiglu",
         "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention",
-        "ns_decode_qkv_attention", "ns_w4_gemv_decode"])
+        "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -147,7 +147,7 @@ def test_decode_qkv_rejects_bad_arguments(k):
 
 def test_decode_attention_workspace_and_rejects(k):
     ws = k.lib.ns_decode_attention_workspace(28, 4, 128, 1024)
-    assert ws == 16 * 28 * 130 * 4  # 64-row splits x heads x (D + max + sum) floats
+    assert ws == 4 * 28 * 130 * 4  # 256-row splits x heads x (D + max + sum) floats
     assert k.lib.ns_decode_attention_workspace(28, 4, 64, 1024) == 0
     assert k.lib.ns_decode_attention_workspace(28, 4, 128, 0) == 0
     assert k.lib.ns_decode_attention_workspace(28, 0, 128, 64) == 0
@@ -165,7 +165,7 @@ def test_decode_attention_workspace_and_rejects(k):
 
     def fused(work_bytes=ws, Hq=28, Hk=4, D=128, L=1024, qkv=P, work=P):
         return k.lib.ns_decode_qkv_attention(qkv, None, P, P, P, P, P, work, work_bytes, Hq, Hk,
-                                             D, L, None)
+                                             D, L, 1, None)
 
     assert fused(work_bytes=ws - 1) == -2
     assert fused(D=64) == -2
@@ -189,3 +189,15 @@ def test_gemv_decode_rejects_bad_arguments(k):
     assert call(N=40, swiglu=1) == -2              # SwiGLU pairs need N % 16 == 0
     assert call(X=P + 8) == -2
     assert call(res=P, nw=P, r=P + 0x1000, res_out=P) == -2  # res_out aliases res
+
+
+def test_gemv_decode_attn_rejects_bad_arguments(k):
+    def call(a=P, work=P, pos=P, L=1024, Hq=28, N=64, K=3584, G=128):
+        return k.lib.ns_w4_gemv_decode_attn(a, work, pos, L, Hq, P, P, P, N, K, G, None)
+
+    assert call(K=3456) == -2          # K != Hq * 128
+    assert call(G=64) == -2
+    assert call(L=0) == -2
+    assert call(work=None) == -2
+    assert call(pos=None) == -2
+    assert call(a=P + 8) == -2

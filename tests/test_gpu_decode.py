@@ -157,15 +157,15 @@ def test_decode_attention_peaked_and_empty(k):
 @pytest.mark.parametrize("with_bias", [True, False])
 def test_decode_qkv_attention(k, Hq, Hk, with_bias):
     """The fused launch against the oracle's bias + RoPE followed by attention over the cache
-    with the new row appended, at positions inside, at the end of and across 64-row splits, at
+    with the new row appended, at positions inside, at the end of and across 256-row splits, at
     the cache's last row, beyond it (no append, attention over the whole cache) and before row
     0 (zeros); one workspace serves every launch in turn."""
-    D, max_len = 128, 300
+    D, max_len = 128, 600
     qn, kn = Hq * D, Hk * D
     work = k.decode_attention_workspace(Hq, Hk, D, max_len)
     freq = R.inv_freq(D, 1000000.0)
     kc, vc = rnd(Hk, max_len, D, seed=20), rnd(Hk, max_len, D, seed=21)
-    for i, pos in enumerate([0, 1, 63, 64, 65, 130, 299, 300, 450, -1]):
+    for i, pos in enumerate([0, 1, 255, 256, 257, 300, 511, 512, 599, 600, 900, -1]):
         print(f"decode_qkv_attention Hq={Hq} Hk={Hk} bias={with_bias} pos={pos}", flush=True)
         # moderate q so that the oracle's and the kernel's q roundings, which may differ by one
         # bf16 ulp in rare elements, move the output by well under the tolerance
@@ -194,6 +194,35 @@ def test_decode_qkv_attention(k, Hq, Hk, with_bias):
         close(out.reshape(-1), R.decode_attention(qr, kc_ref.to(torch.bfloat16),
                                                   vc_ref.to(torch.bfloat16), n, Hq, Hk),
               atol=2e-3)
+
+
+@pytest.mark.parametrize("max_len", [200, 600, 2000])
+def test_gemv_decode_attn_merges_splits(k, max_len):
+    """The o GEMV fed by unmerged attention splits equals the merged attention output times
+    the same weights (one split: the attention's own bf16 output; several: merged in the
+    GEMV's activation load); contexts beyond four splits take the GEMV's batch loop."""
+    Hq, Hk, D, N = 28, 4, 128, 3584
+    qn, kn = Hq * D, Hk * D
+    Wq, S = _w4(N, Hq * D, seed=70)
+    freq = R.inv_freq(D, 1000000.0).to(DEV)
+    work_a = k.decode_attention_workspace(Hq, Hk, D, max_len)
+    work_b = k.decode_attention_workspace(Hq, Hk, D, max_len)
+    kc, vc = rnd(Hk, max_len, D, seed=71), rnd(Hk, max_len, D, seed=72)
+    qkv = rnd(qn + 2 * kn, seed=73, scale=0.5)
+    for pos in sorted({0, 100, 255, 256, max_len // 2, max_len - 1}):
+        print(f"gemv_decode_attn max_len={max_len} pos={pos}", flush=True)
+        p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+        merged = k.decode_qkv_attention(qkv, None, freq, p, kc, vc, Hq, Hk, D, work_a)
+        ref = k.w4_linear(merged, Wq, S, 128)
+        a = torch.empty_like(merged)
+        k.decode_qkv_attention(qkv, None, freq, p, kc, vc, Hq, Hk, D, work_b, out=a,
+                               merge=False)
+        y = k.gemv_decode_attn(a, work_b, p, max_len, Hq, Wq, S)
+        torch.cuda.synchronize()
+        if pos < 256:
+            assert torch.equal(y, ref)  # one split: the same bf16 activation
+        else:  # the two merges round the activation independently: 1 bf16 ulp at most
+            close(y, ref.double().cpu(), rtol=2 ** -6, atol=2e-3 * ref.abs().max().item())
 
 
 # ------------------------------------------------------------------ ns_w4_gemv_decode
