@@ -136,6 +136,17 @@ int ns_w4_gemv_decode_attn(const void* attn_out, const void* work, const int* po
                            int Hq, const void* Wq, const void* S, void* Y, int N, int K, int G,
                            void* stream);
 
+/*
+ * Replaces the reference's bf16 lm_head product for one token, F.linear(h, lm_head)
+ * (python/nanoserve/qwen.py:164, cuBLAS there), with the final norm optionally fused
+ * (qwen.py:161-162): Y [N] bf16 = a . W^T, W [N][K] bf16 row-major, fp32 accumulation, where
+ * the activation a is X [K] bf16, or, if res != NULL, rmsnorm(res + r) * norm_w computed as
+ * ns_rmsnorm does (r may be NULL; res is not written). Returns -2 for K % 8 != 0, K > 8192,
+ * NULL or misaligned pointers (X, res, r, norm_w and W 16-byte aligned).
+ */
+int ns_bf16_gemv(const void* X, const void* res, const void* r, const void* norm_w, float eps,
+                 const void* W, void* Y, int N, int K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

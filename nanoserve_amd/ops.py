@@ -34,6 +34,7 @@ SIGNATURES = {
 }
 SIGNATURES["ns_w4_gemv_decode"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _I32, _I32, _I32,
                                    _I32, _VP]
+SIGNATURES["ns_bf16_gemv"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _I32, _I32, _VP]
 RESTYPES = {"ns_decode_attention_workspace": _SZ}
 
 
@@ -298,4 +299,27 @@ class Kernels:
                                         Wq.data_ptr(), S.data_ptr(), out.data_ptr(), N, K, group,
                                         1 if swiglu else 0, self._stream())
         self._check(rc, "ns_w4_gemv_decode")
+        return out
+
+    def bf16_gemv(self, W, x=None, res=None, r=None, norm_w=None, eps=1e-6, out=None):
+        """One-token bf16 product y [1, N] = a . W^T (W [N, K] bf16), the reference's lm_head
+        F.linear (qwen.py:164); a is x, or with res the fused rmsnorm(res + r) * norm_w."""
+        _require_gpu_tensor(W, "W", torch.bfloat16)
+        if not W.is_contiguous():
+            raise ValueError("W must be contiguous")
+        N, K = W.shape
+        for n, t in (("x", x), ("res", res), ("r", r), ("norm_w", norm_w)):
+            if t is not None:
+                _require_gpu_tensor(t, n, torch.bfloat16)
+                if t.numel() != K or not t.is_contiguous():
+                    raise ValueError(f"{n} must be a contiguous tensor of {K} elements")
+        if out is None:
+            out = torch.empty((1, N), dtype=torch.bfloat16, device=W.device)
+
+        def ptr(t):
+            return None if t is None else t.data_ptr()
+
+        rc = self.lib.ns_bf16_gemv(ptr(x), ptr(res), ptr(r), ptr(norm_w), eps, W.data_ptr(),
+                                   out.data_ptr(), N, K, self._stream())
+        self._check(rc, "ns_bf16_gemv")
         return out

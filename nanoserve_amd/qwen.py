@@ -257,8 +257,8 @@ class Qwen2Runner:
             resid, spare = spare, resid
             k.gemv_decode(*L["wd"], G, x=self.act, out=self.d)
             pending = self.d
-        k.rmsnorm(resid, pending, self.final_norm, eps, out=self.h)
-        torch.mm(self.h, self.lm_head.t(), out=self.logits)
+        k.bf16_gemv(self.lm_head, res=resid, r=pending, norm_w=self.final_norm, eps=eps,
+                    out=self.logits)
 
     def _set_step(self, token, pos: int):
         if self.cache_k is None:

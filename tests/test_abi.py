@@ -35,7 +35,8 @@ def test_header_declares_the_reference_entry_points():
     assert declared_symbols() == sorted([
         "ns_w4_linear", "ns_w4_quantize", "ns_rmsnorm", "ns_rope", "ns_swiglu",
         "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention",
-        "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn"])
+        "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn",
+        "ns_bf16_gemv"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -201,3 +202,15 @@ def test_gemv_decode_attn_rejects_bad_arguments(k):
     assert call(work=None) == -2
     assert call(pos=None) == -2
     assert call(a=P + 8) == -2
+
+
+def test_bf16_gemv_rejects_bad_arguments(k):
+    def call(X=P, res=None, nw=None, N=64, K=256, W=P):
+        return k.lib.ns_bf16_gemv(X, res, None, nw, 1e-6, W, P, N, K, None)
+
+    assert call(K=100) == -2          # K % 8
+    assert call(K=8200) == -2         # K > 8192
+    assert call(N=0) == -2
+    assert call(X=None) == -2
+    assert call(res=P) == -2          # norm without weight
+    assert call(W=P + 8) == -2

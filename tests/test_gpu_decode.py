@@ -320,6 +320,33 @@ def test_gemv_decode_rejects(k):
         k.gemv_decode(Wq, S, 128, res=x, r=x, norm_w=x, res_out=x)
 
 
+# ------------------------------------------------------------------ ns_bf16_gemv (lm_head)
+@pytest.mark.parametrize("N,K", [(152064, 3584), (1000, 896), (77, 8), (300, 8192), (64, 4096)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_bf16_gemv(k, N, K, norm):
+    """bf16 one-token product against float64 on the CPU (every row for small N, 256 sampled
+    rows of the 1.09 GB lm_head), with and without the fused final add + RMSNorm."""
+    print(f"bf16_gemv N={N} K={K} norm={norm}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(80)
+    W = (torch.randn(N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    x, r, w = rnd(K, seed=81, scale=2.0), rnd(K, seed=82), rnd(K, seed=83, scale=0.5)
+    if norm:
+        y = k.bf16_gemv(W, res=x, r=r, norm_w=w, eps=1e-6)
+        _, h = R.rmsnorm(x.reshape(1, -1), r.reshape(1, -1), w, 1e-6)
+        a = R.bf16_round(h).reshape(-1)
+    else:
+        y = k.bf16_gemv(W, x=x)
+        a = x.double().cpu()
+    torch.cuda.synchronize()
+    rows = torch.arange(N) if N <= 4096 else torch.randint(0, N, (256,), generator=torch.Generator().manual_seed(84))
+    ref = W[rows.to(DEV)].double().cpu() @ a
+    out = y.reshape(-1)[rows.to(DEV)].double().cpu()
+    # fp32 accumulation of K products, bf16 output: half a bf16 ulp plus a small floor; with the
+    # norm fused the activation may round one ulp away from the oracle's in rare elements
+    tol = 2 ** -8 * ref.abs() + (2e-3 if norm else 1e-4) * ref.abs().max()
+    assert ((out - ref).abs() <= tol).all(), (out - ref).abs().max().item()
+
+
 # ------------------------------------------------------------------ the runner
 def _hf_model(H, nh, nkv, I, V, layers, seed):
     pytest.importorskip("transformers")
