@@ -210,7 +210,7 @@ __global__ void __launch_bounds__(kBlock)
 // per-head max and sum need two lane swaps instead of a 64-lane reduction per head; the values
 // are a VALU loop, each lane two dims of each of the wave's rows (one 4-byte load per row: the
 // wave reads each 256-byte row whole), probabilities broadcast from LDS.
-constexpr int kAttnWaves = 16;             // waves per attention workgroup, 16 rows each
+constexpr int kAttnWaves = kAttnDecodeChunk / 16;  // waves per attention workgroup, 16 rows each
 constexpr int kAttnBlock = kAttnWaves * kWave;
 constexpr int kChunk = kAttnDecodeChunk;   // cache rows per split
 static_assert(kChunk == 16 * kAttnWaves, "one 16-row score tile per wave");
@@ -237,53 +237,38 @@ __global__ void __launch_bounds__(kAttnBlock)
   __shared__ __attribute__((aligned(16))) uint16_t knew[D];
   __shared__ __attribute__((aligned(16))) uint16_t vnew[D];
 
-  const int pos = *pos_p;
-  const int n = min(pos + 1, max_len);
   const int split = blockIdx.x, g = blockIdx.y;
   const int R = Hq / Hk;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
-  if (n <= 0) {  // no rows: zeros (uniform over the workgroup)
-    if (split == 0)
-      for (int i = tid; i < R * D; i += kAttnBlock) out[(size_t)g * R * D + i] = 0;
-    return;
-  }
   const int start = split * kChunk;
-  if (start >= n) return;  // uniform over the workgroup
-  const int cnt = min(kChunk, n - start);
-  const int nsplit = (n + kChunk - 1) / kChunk;
-  // row `pos` (the token's own) is in this split when it is in the cache at all
-  const bool has_new = kFused && pos < max_len && pos - start < kChunk;
 
-  // ---- issue every load: k (MFMA A fragments), v (two dims per row), then q / bias
+  // ---- issue every load first; none depends on the position, so they overlap its fetch:
+  // k (MFMA A fragments) and v (two dims per row) of the cache rows of this split, then q,
+  // bias and (fused) the token's own k / v heads
   const int r16 = lane & 15, grp = lane >> 4;
   const int krow = 16 * w + r16;  // this lane's k row within the chunk
-  const bool k_valid = krow < cnt;
-  const bool k_is_new = has_new && start + krow == pos;
   u32x4_t ka[4] = {};
-  if (k_valid && !k_is_new) {
+  if (start + krow < max_len) {
     const uint16_t* src = kc + ((size_t)g * max_len + start + krow) * D + 8 * grp;
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) ka[s4] = *reinterpret_cast<const u32x4_t*>(src + 32 * s4);
   }
-  const int rows = min(16, cnt - 16 * w);
+  const int in_cache = min(16, max_len - start - 16 * w);
   const uint16_t* vbase = vc + ((size_t)g * max_len + start + 16 * w) * D + 2 * lane;
   uint32_t vv[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const bool v_is_new = has_new && start + 16 * w + i == pos;
-    vv[i] = i < rows && !v_is_new ? *reinterpret_cast<const uint32_t*>(vbase + (size_t)i * D) : 0u;
-  }
-
+  for (int i = 0; i < 16; ++i)
+    vv[i] = i < in_cache ? *reinterpret_cast<const uint32_t*>(vbase + (size_t)i * D) : 0u;
+  // fused: thread t < 8R: q head t/8, rotation chunk pair t%8; then 8 threads for the k
+  // head's chunk pairs and 16 for the v head's chunks
+  const int nq = 8 * R;
+  const bool is_q = kFused && tid < nq;
+  const bool ld_k = kFused && tid >= nq && tid < nq + 8;
+  const bool ld_v = kFused && tid >= nq + 8 && tid < nq + 24;
+  const int c = is_q ? tid % 8 : tid - nq;
+  u32x4_t a0{}, a1{}, b0{}, b1{};
   if constexpr (kFused) {
-    // thread t < 8R: q head t/8, rotation chunk pair t%8; then 8 threads for the k head's
-    // chunk pairs and 16 for the v head's chunks (only with has_new)
-    const int nq = 8 * R;
-    const bool is_q = tid < nq;
-    const bool is_k = has_new && tid >= nq && tid < nq + 8;
-    const bool is_v = has_new && tid >= nq + 8 && tid < nq + 24;
-    const int c = is_q ? tid % 8 : tid - nq;
-    u32x4_t a0{}, a1{}, b0{}, b1{};
-    if (is_q || is_k) {
+    if (is_q || ld_k) {
       const int off = (is_q ? g * R + tid / 8 : Hq + g) * D + 8 * c;
       a0 = *reinterpret_cast<const u32x4_t*>(q + off);
       a1 = *reinterpret_cast<const u32x4_t*>(q + off + D / 2);
@@ -291,11 +276,42 @@ __global__ void __launch_bounds__(kAttnBlock)
         b0 = *reinterpret_cast<const u32x4_t*>(bias + off);
         b1 = *reinterpret_cast<const u32x4_t*>(bias + off + D / 2);
       }
-    } else if (is_v) {
+    } else if (ld_v) {
       const int off = (Hq + Hk + g) * D + 8 * (tid - nq - 8);
       a0 = *reinterpret_cast<const u32x4_t*>(q + off);
       if (bias) b0 = *reinterpret_cast<const u32x4_t*>(bias + off);
     }
+  } else if (tid < 8 * 16) {  // 16 dims per thread: two 16-byte loads
+    const int h = tid / 8, cc = tid % 8;
+    if (h < R) {
+      const uint16_t* src = q + (size_t)(g * R + h) * D + 16 * cc;
+      a0 = *reinterpret_cast<const u32x4_t*>(src);
+      a1 = *reinterpret_cast<const u32x4_t*>(src + 8);
+    }
+  }
+
+  // ---- the position
+  const int pos = *pos_p;
+  const int n = min(pos + 1, max_len);
+  if (n <= 0) {  // no rows: zeros (uniform over the workgroup)
+    if (split == 0)
+      for (int i = tid; i < R * D; i += kAttnBlock) out[(size_t)g * R * D + i] = 0;
+    return;
+  }
+  if (start >= n) return;  // uniform over the workgroup
+  const int cnt = min(kChunk, n - start);
+  const int nsplit = (n + kChunk - 1) / kChunk;
+  // row `pos` (the token's own) is in this split when it is in the cache at all
+  const bool has_new = kFused && pos < max_len && pos - start < kChunk;
+  const bool k_is_new = has_new && start + krow == pos;
+  const int rows = min(16, cnt - 16 * w);
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (i >= rows) vv[i] = 0u;  // rows past the position: no stale values in the sums
+  const bool is_k = has_new && ld_k;
+  const bool is_v = has_new && ld_v;
+
+  if constexpr (kFused) {
     if (tid < D / 2) {  // the D/2 rotation angles of this position, once per workgroup
       float sn, cs;
       sincosf(static_cast<float>(pos) * inv_freq[tid], &sn, &cs);
@@ -356,14 +372,8 @@ __global__ void __launch_bounds__(kAttnBlock)
       *reinterpret_cast<u32x4_t*>(vc + ((size_t)g * max_len + pos) * D + 8 * cv) = v;
     }
   } else {
-    if (tid < 8 * 16) {  // 16 dims per thread: two 16-byte loads
+    if (tid < 8 * 16) {
       const int h = tid / 8, cc = tid % 8;
-      u32x4_t a0{}, a1{};
-      if (h < R) {
-        const uint16_t* src = q + (size_t)(g * R + h) * D + 16 * cc;
-        a0 = *reinterpret_cast<const u32x4_t*>(src);
-        a1 = *reinterpret_cast<const u32x4_t*>(src + 8);
-      }
       *reinterpret_cast<u32x4_t*>(&qb[h][16 * cc]) = a0;
       *reinterpret_cast<u32x4_t*>(&qb[h][16 * cc + 8]) = a1;
     }

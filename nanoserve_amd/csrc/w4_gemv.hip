@@ -464,7 +464,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   };
   u32x4_t xa[XV], xb[XV], xw[XV];
   // attention merge: this thread's 8 dims (head e / 16) of the first kAttnBatch splits
-  constexpr int kAttnBatch = 4;
+  constexpr int kAttnBatch = NW <= 8 ? 8 : 4;  // registers: fewer with more waves
   float2 aml[kAttnBatch];
   f32x4_t ao[kAttnBatch][2];
   int nsplit = 0;

@@ -196,6 +196,13 @@ def test_decode_qkv_attention(k, Hq, Hk, with_bias):
               atol=2e-3)
 
 
+def _attn_chunk(k):
+    """Cache rows per attention split: the first length at which one more row adds a split
+    to the workspace."""
+    ws = k.lib.ns_decode_attention_workspace
+    return next(n for n in range(1, 4097) if ws(28, 4, 128, n + 1) > ws(28, 4, 128, n))
+
+
 @pytest.mark.parametrize("max_len", [200, 600, 2000])
 def test_gemv_decode_attn_merges_splits(k, max_len):
     """The o GEMV fed by unmerged attention splits equals the merged attention output times
@@ -209,7 +216,7 @@ def test_gemv_decode_attn_merges_splits(k, max_len):
     work_b = k.decode_attention_workspace(Hq, Hk, D, max_len)
     kc, vc = rnd(Hk, max_len, D, seed=71), rnd(Hk, max_len, D, seed=72)
     qkv = rnd(qn + 2 * kn, seed=73, scale=0.5)
-    for pos in sorted({0, 100, 255, 256, max_len // 2, max_len - 1}):
+    for pos in sorted({0, 100, 127, 128, 255, 256, max_len // 2, max_len - 1}):
         print(f"gemv_decode_attn max_len={max_len} pos={pos}", flush=True)
         p = torch.tensor([pos], dtype=torch.int32, device=DEV)
         merged = k.decode_qkv_attention(qkv, None, freq, p, kc, vc, Hq, Hk, D, work_a)
@@ -219,7 +226,7 @@ def test_gemv_decode_attn_merges_splits(k, max_len):
                                merge=False)
         y = k.gemv_decode_attn(a, work_b, p, max_len, Hq, Wq, S)
         torch.cuda.synchronize()
-        if pos < 256:
+        if pos < _attn_chunk(k):
             assert torch.equal(y, ref)  # one split: the same bf16 activation
         else:  # the two merges round the activation independently: 1 bf16 ulp at most
             close(y, ref.double().cpu(), rtol=2 ** -6, atol=2e-3 * ref.abs().max().item())
