@@ -224,6 +224,42 @@ def main():
                 "eager_ms_per_token": round(ms_eager, 3), "context": ctx, "logits_finite": finite,
                 "timing": f"median of 5 x {reps} graph replays, hip events"}
 
+    def packed_sets():
+        """The same M = 1 and M = 8 sets on the packed tile format (ns_w4_repack once, then
+        ns_w4_linear_packed) for the layers with K <= 4096, where the packed kernel keeps the
+        activation in registers; the down layer (K = 18944) runs ns_w4_linear in the set."""
+        pk = {name: [kern.w4_repack(wq, s, G) for wq, s in dev_w[name]] for name, _, _ in layers}
+        torch.cuda.synchronize()
+        res = {}
+        for M, xs in ((1, x1), (8, x8)):
+            ok = {name: K <= 4096 for name, N, K in layers}
+
+            def run(i, which=None, M=M, xs=xs, ok=ok):
+                for name, N, K in layers:
+                    if which is not None and name != which:
+                        continue
+                    if ok[name]:
+                        kern.w4_linear_packed(xs[name], *pk[name][i % copies], N, G)
+                    else:
+                        kern.w4_linear(xs[name], *dev_w[name][i % copies], G)
+
+            for name, N, K in layers:
+                g = graph_of(lambda i, name=name: run(i, which=name), n_launch)
+                time_graph(g)
+                ms = statistics.median(time_graph(g) for _ in range(3)) / n_launch
+                b = synth.gemv_bytes(M, N, K, G)
+                res[f"{name}_m{M}"] = {"us": round(ms * 1e3, 3), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
+                                       "packed": ok[name]}
+            g = graph_of(lambda i: run(i), 4 * copies)
+            time_graph(g)
+            ms = statistics.median(time_graph(g) for _ in range(3)) / (4 * copies)
+            b = sum(synth.gemv_bytes(M, N, K, G) for _, N, K in layers)
+            res[f"set_m{M}"] = {"us": round(ms * 1e3, 3), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
+                                "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del pk
+        torch.cuda.empty_cache()
+        return res
+
     if args.gemm_only:
         print(json.dumps({"config4_gemm": gemm_set()}), flush=True)
         return
@@ -309,6 +345,7 @@ def main():
         extra["config1_gate_m1"] = {"us": round(ms1 * 1e3, 3), "gbs": round(b1 / (ms1 * 1e-3) / 1e9, 1)}
         del c1w, wq0, s0
 
+        extra["packed_format"] = packed_sets()
         extra["config4_gemm"] = gemm_set()
         extra["config5_decode"] = decode_step()
 

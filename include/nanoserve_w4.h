@@ -53,6 +53,31 @@ int ns_w4_quantize(const void* W, void* Wq, void* S, int N, int K, int G, void* 
 int ns_w4_linear(const void* X, const void* Wq, const void* S, void* Y, int M, int N, int K,
                  int G, void* stream);
 
+/*
+ * No counterpart in the reference (its README:149-151 names a Marlin-style pre-shuffled weight
+ * format as the next step). Rewrites (Wq, S) of ns_w4_quantize's format, G == 128, into the
+ * packed tile format ns_w4_linear_packed reads: tiles of 16 rows x 128 k, tile (t, c) at
+ * Wp + 1024 * (t * (K/128) + c) bytes and Sp + 32 * (t * (K/128) + c) bytes; within a tile the
+ * 16-byte run of lane l holds row 16t + l%16, k = 128c + 32s + 8(l/16) + e in word s, nibbles
+ * in the order e = 0 2 4 6 1 3 5 7; scales in row order. Sizes: Wp ceil(N/16) * (K/128) * 1024
+ * bytes, Sp ceil(N/16) * (K/128) * 32 bytes; rows past N are zero. Returns -2 for G != 128,
+ * K % 128 != 0, a packed size of 2 GiB or more, NULL or misaligned pointers (Wp, Sp 16-byte).
+ */
+int ns_w4_repack(const void* Wq, const void* S, void* Wp, void* Sp, int N, int K, int G,
+                 void* stream);
+
+/*
+ * No counterpart in the reference. ns_w4_linear for M = 1..16 on packed weights (ns_w4_repack):
+ * Y [M][N] bf16 (RNE) = X [M][K] bf16 . deq(W)^T with fp32 accumulation, the same exact
+ * dequantisation and products as ns_w4_linear's decode GEMV (fp32 sums over k-groups in another
+ * order: outputs agree with ns_w4_linear's to one bf16 ulp, most bit for bit). Returns -2
+ * for M outside 1..16, G != 128, K % 128 != 0, K > 20480, K > 4096 when M * K / 128 * 256 bytes
+ * of activation exceed 96 KiB, a packed size of 2 GiB or more, NULL or misaligned pointers (X,
+ * Wp, Sp 16-byte aligned).
+ */
+int ns_w4_linear_packed(const void* X, const void* Wp, const void* Sp, void* Y, int M, int N,
+                        int K, int G, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,8 @@ SIGNATURES = {
 SIGNATURES["ns_w4_gemv_decode"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _I32, _I32, _I32,
                                    _I32, _VP]
 SIGNATURES["ns_bf16_gemv"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _I32, _I32, _VP]
+SIGNATURES["ns_w4_repack"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _VP]
+SIGNATURES["ns_w4_linear_packed"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
 RESTYPES = {"ns_decode_attention_workspace": _SZ}
 
 
@@ -322,4 +324,35 @@ class Kernels:
         rc = self.lib.ns_bf16_gemv(ptr(x), ptr(res), ptr(r), ptr(norm_w), eps, W.data_ptr(),
                                    out.data_ptr(), N, K, self._stream())
         self._check(rc, "ns_bf16_gemv")
+        return out
+
+    # ------------------------------------------------------------------ packed tile format
+    def w4_repack(self, Wq, S, group=128):
+        """(Wq [N, K/8] int32, S [N, K/128] bf16) -> packed tiles (Wp int32 [ceil(N/16), K/128,
+        256], Sp bf16 [ceil(N/16), K/128, 16]) for w4_linear_packed (include/nanoserve_w4.h)."""
+        _require_gpu_tensor(Wq, "Wq", torch.int32)
+        _require_gpu_tensor(S, "S", torch.bfloat16)
+        N, K = Wq.shape[0], Wq.shape[1] * 8
+        NT, C = (N + 15) // 16, K // 128
+        Wp = torch.empty((NT, C, 256), dtype=torch.int32, device=Wq.device)
+        Sp = torch.empty((NT, C, 16), dtype=torch.bfloat16, device=Wq.device)
+        rc = self.lib.ns_w4_repack(Wq.contiguous().data_ptr(), S.contiguous().data_ptr(),
+                                   Wp.data_ptr(), Sp.data_ptr(), N, K, group, self._stream())
+        self._check(rc, "ns_w4_repack")
+        return Wp, Sp
+
+    def w4_linear_packed(self, x, Wp, Sp, N, group=128, out=None):
+        """x [M, K] bf16 (M <= 16) -> y [M, N] bf16, as w4_linear on the packed weights of
+        w4_repack (agreeing with it to one bf16 ulp)."""
+        _require_gpu_tensor(x, "x", torch.bfloat16)
+        _require_gpu_tensor(Wp, "Wp", torch.int32)
+        _require_gpu_tensor(Sp, "Sp", torch.bfloat16)
+        M, K = x.shape
+        if Wp.shape[0] * 16 < N or Wp.shape[1] * 128 != K:
+            raise ValueError("packed weights do not match N and x's K")
+        if out is None:
+            out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+        rc = self.lib.ns_w4_linear_packed(x.contiguous().data_ptr(), Wp.data_ptr(), Sp.data_ptr(),
+                                          out.data_ptr(), M, N, K, group, self._stream())
+        self._check(rc, "ns_w4_linear_packed")
         return out

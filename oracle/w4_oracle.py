@@ -192,3 +192,45 @@ def torch_cpu_linear(x, Wq, S, G: int = 128):
     w = (q.reshape(N, K).to(torch.float32) - 8.0)
     w = w.view(N, K // G, G) * S.to(torch.float32).unsqueeze(-1)
     return x.to(torch.float32) @ w.view(N, K).t()
+
+
+# ----------------------------------------------------------------- packed tile format
+def pack_word_nibbles(w: np.ndarray) -> np.ndarray:
+    """Element e of a natural-order word (nibble e) -> nibble position e//2 + 4*(e%2): the
+    packed order e0 e2 e4 e6 e1 e3 e5 e7 of ns_w4_repack (include/nanoserve_w4.h)."""
+    w = np.asarray(w, dtype=np.uint32)
+    out = np.zeros_like(w)
+    for e in range(8):
+        p = e // 2 + 4 * (e % 2)
+        out |= ((w >> np.uint32(4 * e)) & np.uint32(0xF)) << np.uint32(4 * p)
+    return out
+
+
+def unpack_word_nibbles(w: np.ndarray) -> np.ndarray:
+    """Inverse of pack_word_nibbles."""
+    w = np.asarray(w, dtype=np.uint32)
+    out = np.zeros_like(w)
+    for e in range(8):
+        p = e // 2 + 4 * (e % 2)
+        out |= ((w >> np.uint32(4 * p)) & np.uint32(0xF)) << np.uint32(4 * e)
+    return out
+
+
+def repack_tiles(Wq: np.ndarray, S: np.ndarray):
+    """The packed tile format of ns_w4_repack, restated with numpy (G = 128): tile (t, c) =
+    rows 16t..16t+15 x k 128c..128c+127; within a tile, lane l = 16 kg + j holds four words
+    s = 0..3 of row 16t + j at word index 16c + 4s + kg of the row; tiles t-major; rows past N
+    are zero. Returns (Wp uint32 [NT*C*256], Sp uint16 [NT*C*16])."""
+    Wq = np.asarray(Wq, dtype=np.uint32)
+    S = np.asarray(S, dtype=np.uint16)
+    N, KW = Wq.shape
+    C = KW // 16
+    NT = (N + 15) // 16
+    Wpad = np.zeros((NT * 16, KW), dtype=np.uint32)
+    Wpad[:N] = Wq
+    Spad = np.zeros((NT * 16, C), dtype=np.uint16)
+    Spad[:N] = S
+    tiles = Wpad.reshape(NT, 16, C, 4, 4).transpose(0, 2, 4, 1, 3)  # [t][c][kg][j][s]
+    Wp = pack_word_nibbles(tiles.reshape(-1))
+    Sp = Spad.reshape(NT, 16, C).transpose(0, 2, 1).reshape(-1)
+    return np.ascontiguousarray(Wp), np.ascontiguousarray(Sp)

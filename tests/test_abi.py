@@ -33,7 +33,8 @@ def test_header_declares_the_reference_entry_points():
     # the reference's W4 and fused-op entry points (csrc/nanoserve_ops.cu:20-90), plus the
     # decode-step attention operators the reference does with PyTorch ops
     assert declared_symbols() == sorted([
-        "ns_w4_linear", "ns_w4_quantize", "ns_rmsnorm", "ns_rope", "ns_swiglu",
+        "ns_w4_linear", "ns_w4_quantize", "ns_w4_repack", "ns_w4_linear_packed",
+        "ns_rmsnorm", "ns_rope", "ns_swiglu",
         "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention",
         "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn",
         "ns_bf16_gemv"])
@@ -214,3 +215,14 @@ def test_bf16_gemv_rejects_bad_arguments(k):
     assert call(X=None) == -2
     assert call(res=P) == -2          # norm without weight
     assert call(W=P + 8) == -2
+
+
+def test_packed_entry_points_reject_bad_arguments(k):
+    assert k.lib.ns_w4_repack(P, P, P, P, 64, 256, 64, None) == -2      # G != 128
+    assert k.lib.ns_w4_repack(P, P, P, P, 64, 200, 128, None) == -2     # K % 128
+    assert k.lib.ns_w4_repack(P, P, P + 8, P, 64, 256, 128, None) == -2
+    assert k.lib.ns_w4_linear_packed(P, P, P, P, 17, 64, 256, 128, None) == -2   # M > 16
+    assert k.lib.ns_w4_linear_packed(P, P, P, P, 0, 64, 256, 128, None) == -2
+    assert k.lib.ns_w4_linear_packed(P, P, P, P, 1, 64, 20608, 128, None) == -2  # K > 20480
+    assert k.lib.ns_w4_linear_packed(P, P, P, P, 8, 64, 18944, 128, None) == -2  # LDS budget
+    assert k.lib.ns_w4_linear_packed(P + 8, P, P, P, 1, 64, 256, 128, None) == -2

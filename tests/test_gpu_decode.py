@@ -354,6 +354,46 @@ def test_bf16_gemv(k, N, K, norm):
     assert ((out - ref).abs() <= tol).all(), (out - ref).abs().max().item()
 
 
+# ------------------------------------------------------------------ packed tile format
+@pytest.mark.parametrize("N,K", [(4608, 3584), (40, 384), (3584, 18944), (8960, 1536)])
+def test_repack_matches_oracle(k, N, K):
+    print(f"repack N={N} K={K}", flush=True)
+    Wq, S = _w4(N, K, seed=90)
+    Wp, Sp = k.w4_repack(Wq, S)
+    torch.cuda.synchronize()
+    wp_ref, sp_ref = O.repack_tiles(Wq.cpu().numpy().view("uint32"),
+                                    S.cpu().view(torch.int16).numpy().view("uint16"))
+    assert (Wp.cpu().numpy().view("uint32").reshape(-1) == wp_ref).all()
+    assert (Sp.cpu().view(torch.int16).numpy().view("uint16").reshape(-1) == sp_ref).all()
+
+
+@pytest.mark.parametrize("N,K", [(4608, 3584), (3584, 3584), (37888, 3584), (8960, 1536),
+                                 (40, 384), (3584, 18944), (100, 4096)])
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 16])
+def test_w4_linear_packed_equals_w4_linear(k, N, K, M):
+    """The packed GEMV computes what ns_w4_linear computes (same exact dequantisation and
+    products; ns_w4_linear is checked against the oracle in test_gpu_parity.py); the fp32 sums
+    over k-groups run in another order, so outputs agree to one bf16 ulp (most bit for bit)."""
+    if K > 4096 and M * (K // 128) * 256 > 96 * 1024:
+        pytest.skip("activation rows beyond the packed kernel's LDS budget (rejected, -2)")
+    print(f"w4_linear_packed N={N} K={K} M={M}", flush=True)
+    Wq, S = _w4(N, K, seed=91)
+    Wp, Sp = k.w4_repack(Wq, S)
+    x = rnd(M, K, seed=92)
+    y = k.w4_linear_packed(x, Wp, Sp, N)
+    ref = k.w4_linear(x, Wq, S, 128) if M <= 8 else torch.cat(
+        [k.w4_linear(x[:8], Wq, S, 128), k.w4_linear(x[8:], Wq, S, 128)])
+    torch.cuda.synchronize()
+    # near-zero outputs (cancelling sums) get an absolute floor from the output scale
+    close(y, ref.double().cpu(), rtol=2 ** -7, atol=2e-5 * ref.abs().max().item())
+    assert (y == ref).float().mean().item() > 0.9
+    # and the packed output against the oracle's float64 product directly
+    xb = x.cpu().view(torch.int16).numpy().view("uint16")
+    ref64 = torch.from_numpy(O.linear_f64(xb, Wq.cpu().numpy().view("uint32"),
+                                          S.cpu().view(torch.int16).numpy().view("uint16"), 128))
+    close(y, ref64, rtol=2 ** -8, atol=1e-5 * ref64.abs().max().item())
+
+
 # ------------------------------------------------------------------ the runner
 def _hf_model(H, nh, nkv, I, V, layers, seed):
     pytest.importorskip("transformers")

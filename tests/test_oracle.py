@@ -152,3 +152,41 @@ def test_quantizer_special_groups(oracle):
     assert ((Wq[1, 0] >> 20) & 0xF) == 1
     with pytest.raises(ValueError):
         oracle.quantize(Wb, 48)                                # G % 32 != 0 -> rejected
+
+
+# ----------------------------------------------------------------- packed tile format
+def test_pack_word_nibbles_closed_form():
+    # nibbles 0..7 in natural order -> positions 0,4,1,5,2,6,3,7: 0x75316420
+    from oracle.w4_oracle import pack_word_nibbles, unpack_word_nibbles
+    w = np.array([0x76543210], dtype=np.uint32)
+    assert pack_word_nibbles(w)[0] == 0x75316420
+    # (packed >> 4i) & 0x000F000F holds elements 2i and 2i+1 in its two halves
+    p = int(pack_word_nibbles(w)[0])
+    for i in range(4):
+        v = (p >> (4 * i)) & 0x000F000F
+        assert (v & 0xF, v >> 16) == (2 * i, 2 * i + 1)
+    rng = np.random.default_rng(5)
+    r = rng.integers(0, 2 ** 32, size=1000, dtype=np.uint64).astype(np.uint32)
+    assert np.array_equal(unpack_word_nibbles(pack_word_nibbles(r)), r)
+
+
+def test_repack_tiles_places_every_word_once():
+    from oracle.w4_oracle import repack_tiles, unpack_word_nibbles
+    N, K = 40, 384  # N not a multiple of 16
+    rng = np.random.default_rng(6)
+    Wq = rng.integers(0, 2 ** 32, size=(N, K // 8), dtype=np.uint64).astype(np.uint32)
+    S = rng.integers(0, 2 ** 16, size=(N, K // 128), dtype=np.uint64).astype(np.uint16)
+    Wp, Sp = repack_tiles(Wq, S)
+    C, NT = K // 128, (N + 15) // 16
+    assert Wp.size == NT * C * 256 and Sp.size == NT * C * 16
+    words = unpack_word_nibbles(Wp).reshape(NT, C, 64, 4)
+    for t in range(NT):
+        for c in range(C):
+            for lane in range(64):
+                j, kg = lane % 16, lane // 16
+                row = 16 * t + j
+                for s in range(4):
+                    want = Wq[row, 16 * c + 4 * s + kg] if row < N else 0
+                    assert words[t, c, lane, s] == want
+                if s == 3 and lane < 16:
+                    assert Sp[(t * C + c) * 16 + j] == (S[row, c] if row < N else 0)
