@@ -224,6 +224,44 @@ def main():
                 "eager_ms_per_token": round(ms_eager, 3), "context": ctx, "logits_finite": finite,
                 "timing": f"median of 5 x {reps} graph replays, hip events"}
 
+    def gptq_set():
+        """The calibrated quantizer (ns_w4_gptq) on the gate_up and down layers: one call after a
+        warm-up call, hip events; the float64 factor U separately (host clock, synchronised);
+        quality as the layer's output error on calibration rows through ns_w4_linear relative to
+        round to nearest's. Calibration activations: a rank-32 component plus noise."""
+        from nanoserve_amd import gptq as gq
+
+        res = {}
+        gen = torch.Generator(device=dev).manual_seed(5)
+        for name, N, K in layers:
+            if name not in ("gate_up", "down"):
+                continue
+            W = (torch.randn(N, K, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+            X = (torch.randn(512, 32, device=dev, generator=gen)
+                 @ torch.randn(32, K, device=dev, generator=gen) / 32 ** 0.5
+                 + 0.3 * torch.randn(512, K, device=dev, generator=gen))
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            U, _ = gq.hessian_factor(gq.hessian(X))
+            torch.cuda.synchronize()
+            t_factor = time.perf_counter() - t0
+            kern.w4_gptq(W, U, G)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            Wq, S = kern.w4_gptq(W, U, G)
+            e1.record()
+            torch.cuda.synchronize()
+            Wr, Sr = kern.w4_quantize(W, G)
+            xb = X[:128].to(torch.bfloat16)
+            ref = xb.float() @ W.float().t()
+            err_g = float((kern.w4_linear(xb, Wq, S, G).float() - ref).norm())
+            err_r = float((kern.w4_linear(xb, Wr, Sr, G).float() - ref).norm())
+            res[name] = {"shape": [N, K], "ms": round(e0.elapsed_time(e1), 2),
+                         "factor_s": round(t_factor, 3), "err_vs_rtn": round(err_g / err_r, 4)}
+            del W, X, U, Wq, S, Wr, Sr
+        torch.cuda.empty_cache()
+        return res
+
     def packed_sets():
         """The same M = 1 and M = 8 sets on the packed tile format (ns_w4_repack once, then
         ns_w4_linear_packed) for the layers with K <= 4096, where the packed kernel keeps the
@@ -348,6 +386,7 @@ def main():
         extra["packed_format"] = packed_sets()
         extra["config4_gemm"] = gemm_set()
         extra["config5_decode"] = decode_step()
+        extra["gptq"] = gptq_set()
 
 
     # ---------------- CPU baseline (PyTorch CPU dequant + fp32 matmul), full M=1 set

@@ -19,6 +19,8 @@
 #ifndef NANOSERVE_W4_H
 #define NANOSERVE_W4_H
 
+#include <stddef.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -77,6 +79,30 @@ int ns_w4_repack(const void* Wq, const void* S, void* Wp, void* Sp, int N, int K
  */
 int ns_w4_linear_packed(const void* X, const void* Wp, const void* Sp, void* Y, int M, int N,
                         int K, int G, void* stream);
+
+/*
+ * Bytes of fp32 workspace ns_w4_gptq needs for N rows (128 * N * 4); 0 for N <= 0.
+ */
+size_t ns_w4_gptq_workspace(int N);
+
+/*
+ * No counterpart in the reference's C ABI: the calibrated quantizer its README.md:233-235 names
+ * as the next step after ns_w4_quantize (GPTQ, Frantar et al. 2022, columns in natural order,
+ * one scale per row and 128-column group). Output format exactly as ns_w4_quantize's.
+ *   W [N][K] fp32: the weights, overwritten (working memory; its contents afterwards are
+ *   unspecified). U [K][K] fp32: the upper Cholesky factor of the damped inverse Hessian of the
+ *   layer's calibration activations (U^T U = (2 X^T X / T + damping)^-1), computed by the caller;
+ *   only its upper triangle is read. work: ns_w4_gptq_workspace(N) bytes of device memory.
+ * Column i of each row is quantized with the round-to-nearest rule of ns_w4_quantize, the group
+ * scale taken from the row's group values as they stand when the group starts; its error
+ * e = (w_i - (q - 8) s) / U[i][i] updates each later column j as w_j <- fma(-e, U[i][j], w_j),
+ * the updates of each w_j applied in increasing i. With U diagonal and bf16-valued W, (Wq, S)
+ * equal ns_w4_quantize's.
+ * Returns -2 for G != 128, K % 128 != 0, N <= 0, work_bytes too small, NULL or misaligned
+ * pointers (W, U, Wq, work 16-byte aligned).
+ */
+int ns_w4_gptq(void* W, const void* U, void* Wq, void* S, void* work, size_t work_bytes, int N,
+               int K, int G, void* stream);
 
 #ifdef __cplusplus
 }

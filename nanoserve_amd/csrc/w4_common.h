@@ -95,4 +95,14 @@ __device__ __forceinline__ float wave_max(float v) {
 // silu(g) * u, the reference's SwiGLU (kernels/fused/swiglu.cuh:8), in fp32.
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.f + __expf(-g)) * u; }
 
+// Round half to even, then a saturating int32 conversion with NaN -> 0 (the semantics of the
+// reference's __float2int_rn), written out so no out-of-range conversion is left undefined.
+__device__ __forceinline__ int f2i_rn(float x) {
+  if (!(x == x)) return 0;
+  const float r = __builtin_rintf(x);
+  if (r >= 2147483648.f) return 0x7fffffff;
+  if (r < -2147483648.f) return (int)0x80000000u;
+  return (int)r;
+}
+
 }  // namespace ns

@@ -17,16 +17,6 @@ namespace {
 
 __device__ __forceinline__ float abs_bf16(uint32_t h) { return bf16_bits_to_f32(h & 0x7fffu); }
 
-// Round half to even, then a saturating int32 conversion with NaN -> 0 (the semantics of the
-// reference's __float2int_rn), written out so no out-of-range conversion is left undefined.
-__device__ __forceinline__ int f2i_rn(float x) {
-  if (!(x == x)) return 0;
-  const float r = __builtin_rintf(x);
-  if (r >= 2147483648.f) return 0x7fffffff;
-  if (r < -2147483648.f) return (int)0x80000000u;
-  return (int)r;
-}
-
 template <bool kShuffle>
 __global__ __launch_bounds__(256) void w4_quantize_kernel(const uint16_t* __restrict__ W,
                                                           uint32_t* __restrict__ Wq,

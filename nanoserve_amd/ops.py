@@ -37,7 +37,9 @@ SIGNATURES["ns_w4_gemv_decode"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _VP, _VP,
 SIGNATURES["ns_bf16_gemv"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _I32, _I32, _VP]
 SIGNATURES["ns_w4_repack"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_w4_linear_packed"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
-RESTYPES = {"ns_decode_attention_workspace": _SZ}
+SIGNATURES["ns_w4_gptq_workspace"] = [_I32]
+SIGNATURES["ns_w4_gptq"] = [_VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32, _VP]
+RESTYPES = {"ns_decode_attention_workspace": _SZ, "ns_w4_gptq_workspace": _SZ}
 
 
 def _require_gpu_tensor(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
@@ -92,6 +94,29 @@ class Kernels:
         rc = self.lib.ns_w4_quantize(W.data_ptr(), Wq.data_ptr(), S.data_ptr(), N, K, group,
                                      self._stream())
         self._check(rc, "ns_w4_quantize")
+        return Wq, S
+
+    def w4_gptq(self, W, U, group=128):
+        """Calibrated quantization (not in the reference, whose README.md:233-235 names it as
+        the next step): W [N, K] (any float dtype) and U [K, K] fp32, the upper Cholesky factor
+        of the layer's damped inverse Hessian (``nanoserve_amd.gptq.hessian_factor``) ->
+        (Wq int32 [N, K // 8], S bf16 [N, K // group]) in w4_quantize's format. W is not
+        modified (the kernels work on an fp32 copy)."""
+        if not isinstance(W, torch.Tensor) or not W.is_cuda:
+            raise ValueError("W must be a CUDA (HIP) tensor")
+        _require_gpu_tensor(U, "U", torch.float32)
+        N, K = W.shape
+        if tuple(U.shape) != (K, K):
+            raise ValueError(f"U must be [{K}, {K}], got {tuple(U.shape)}")
+        Wf = W.to(torch.float32).contiguous().clone()
+        U = U.contiguous()
+        Wq = torch.empty((N, K // 8), dtype=torch.int32, device=W.device)
+        S = torch.empty((N, K // group), dtype=torch.bfloat16, device=W.device)
+        nbytes = self.lib.ns_w4_gptq_workspace(N)
+        work = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=W.device)
+        rc = self.lib.ns_w4_gptq(Wf.data_ptr(), U.data_ptr(), Wq.data_ptr(), S.data_ptr(),
+                                 work.data_ptr(), work.numel(), N, K, group, self._stream())
+        self._check(rc, "ns_w4_gptq")
         return Wq, S
 
     def w4_linear(self, x, Wq, S, group=128, out=None):

@@ -14,6 +14,9 @@
  *   orc_dequant_bf16    kernels/quant/w4a16.cuh:190-198 (GEMM staging: RNE of the above)
  *   orc_linear_f64      bench/bench_w4a16.cu:163-173 (double accumulation)
  *   orc_linear_w4_f64   same, dequantizing on the fly (no N*K float buffer)
+ *   orc_gptq            GPTQ (Frantar et al. 2022, Algorithm 1, natural column order) with the
+ *                       quantization rule of kernels/quant/w4a16.cuh:272-297; the reference has
+ *                       no calibrated quantizer (README.md:233-235 names it as next)
  *   orc_gemv_ref_order  kernels/quant/w4a16.cuh:21-24, 42-95 (<M,1,float>: per-lane FMA
  *                       order and xor-shuffle tree of the reference GEMV, fp32)
  *
@@ -196,4 +199,41 @@ void orc_gemv_ref_order(const uint16_t* X, const uint32_t* Wq, const uint16_t* S
       }
       Y[(size_t)m * N + n] = lane_acc[0];
     }
+}
+
+/* GPTQ, unblocked and sequential, one row at a time (rows are independent). W [N][K] fp32 is
+ * updated in place; U [K][K] fp32 is the upper Cholesky factor of the damped inverse Hessian.
+ * For each group g, the scale comes from the row's group values as they stand when the group
+ * starts, by the rule of orc_quantize: s = bf16_rne(max|w| / 7) (1 for an all-zero group).
+ * Then for each column i of the group: q = clamp(rint(w_i / s) + 8, 0, 15) (saturating
+ * conversion, NaN -> 0), e = fma(-(q - 8), s, w_i) / U[i][i] (the product is exact), and
+ * w_j = fma(-e, U[i][j], w_j) for every j > i, in that order. Afterwards W[n][i] holds the value
+ * column i had when it was quantized. Codes and scales in the format of orc_quantize. */
+int orc_gptq(float* W, const float* U, uint32_t* Wq, uint16_t* S, int N, int K, int G) {
+  if (G <= 0 || K % G || G % 8) return -1;
+  const int KG = K / G;
+  for (int n = 0; n < N; ++n) {
+    float* w = W + (size_t)n * K;
+    for (int g = 0; g < KG; ++g) {
+      float mx = 0.f;
+      for (int i = g * G; i < (g + 1) * G; ++i) mx = fmaxf(mx, fabsf(w[i]));
+      const uint16_t sb = orc_bf16_rne(mx > 0.f ? mx / 7.f : 1.f);
+      const float sf = orc_bf16_to_f32(sb);
+      S[(size_t)n * KG + g] = sb;
+      uint32_t word = 0;
+      for (int i = g * G; i < (g + 1) * G; ++i) {
+        int32_t q = (int32_t)((uint32_t)f2i_rn_sat(w[i] / sf) + 8u);
+        q = q < 0 ? 0 : (q > 15 ? 15 : q);
+        word |= (uint32_t)q << (4 * (i & 7));
+        if ((i & 7) == 7) {
+          Wq[(size_t)n * (K / 8) + i / 8] = word;
+          word = 0;
+        }
+        const float e = fmaf(-(float)(q - 8), sf, w[i]) / U[(size_t)i * K + i];
+        const float* ur = U + (size_t)i * K;
+        for (int j = i + 1; j < K; ++j) w[j] = fmaf(-e, ur[j], w[j]);
+      }
+    }
+  }
+  return 0;
 }

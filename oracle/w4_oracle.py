@@ -50,6 +50,7 @@ def lib():
             "orc_linear_f64": ([vp, vp, vp, i32, i32, i32], None),
             "orc_linear_w4_f64": ([vp, vp, vp, vp, i32, i32, i32, i32, i32], None),
             "orc_gemv_ref_order": ([vp, vp, vp, vp, i32, i32, i32, i32], None),
+            "orc_gptq": ([vp, vp, vp, vp, i32, i32, i32], ctypes.c_int),
         }
         for name, (args, res) in sigs.items():
             fn = getattr(L, name)
@@ -96,6 +97,22 @@ def quantize(W: np.ndarray, G: int = 128):
     if rc != 0:
         raise ValueError(f"orc_quantize rejected K={K}, G={G}")
     return Wq, S
+
+
+def gptq(W: np.ndarray, U: np.ndarray, G: int = 128):
+    """GPTQ restatement (orc_gptq in w4_oracle.c). W [N, K] float32 weights, U [K, K] float32
+    upper Cholesky factor of the damped inverse Hessian -> (Wq uint32 [N, K/8], S uint16
+    [N, K/G], Wpre float32 [N, K]: the value each column had when it was quantized)."""
+    Wpre = np.array(W, dtype=np.float32, order="C", copy=True)
+    U = np.ascontiguousarray(U, dtype=np.float32)
+    N, K = Wpre.shape
+    assert U.shape == (K, K)
+    Wq = np.empty((N, K // 8), dtype=np.uint32)
+    S = np.empty((N, max(K // G, 1)), dtype=np.uint16)
+    rc = lib().orc_gptq(_p(Wpre), _p(U), _p(Wq), _p(S), N, K, G)
+    if rc != 0:
+        raise ValueError(f"orc_gptq rejected K={K}, G={G}")
+    return Wq, S, Wpre
 
 
 def dequant_f32(Wq: np.ndarray, S: np.ndarray, G: int = 128) -> np.ndarray:

@@ -37,7 +37,7 @@ def test_header_declares_the_reference_entry_points():
         "ns_rmsnorm", "ns_rope", "ns_swiglu",
         "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention",
         "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn",
-        "ns_bf16_gemv"])
+        "ns_bf16_gemv", "ns_w4_gptq_workspace", "ns_w4_gptq"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -226,3 +226,17 @@ def test_packed_entry_points_reject_bad_arguments(k):
     assert k.lib.ns_w4_linear_packed(P, P, P, P, 1, 64, 20608, 128, None) == -2  # K > 20480
     assert k.lib.ns_w4_linear_packed(P, P, P, P, 8, 64, 18944, 128, None) == -2  # LDS budget
     assert k.lib.ns_w4_linear_packed(P + 8, P, P, P, 1, 64, 256, 128, None) == -2
+
+
+def test_gptq_workspace_and_rejects(k):
+    assert k.lib.ns_w4_gptq_workspace(0) == 0
+    assert k.lib.ns_w4_gptq_workspace(-3) == 0
+    assert k.lib.ns_w4_gptq_workspace(37888) == 128 * 37888 * 4
+    ws = 128 * 64 * 4
+    assert k.lib.ns_w4_gptq(P, P, P, P, P, ws, 64, 256, 64, None) == -2      # G != 128
+    assert k.lib.ns_w4_gptq(P, P, P, P, P, ws, 64, 200, 128, None) == -2     # K % 128
+    assert k.lib.ns_w4_gptq(P, P, P, P, P, ws, 0, 256, 128, None) == -2      # N <= 0
+    assert k.lib.ns_w4_gptq(P, P, P, P, P, ws - 4, 64, 256, 128, None) == -2  # small workspace
+    assert k.lib.ns_w4_gptq(P + 8, P, P, P, P, ws, 64, 256, 128, None) == -2  # W misaligned
+    assert k.lib.ns_w4_gptq(P, P + 4, P, P, P, ws, 64, 256, 128, None) == -2  # U misaligned
+    assert k.lib.ns_w4_gptq(P, P, P, P, None, ws, 64, 256, 128, None) == -2
