@@ -35,6 +35,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from . import gptq
 from .ops import Kernels
 
 
@@ -87,6 +88,34 @@ def interleave_gate_up(Wq: torch.Tensor, S: torch.Tensor):
         return t.view(2, N // 16, 8, t.shape[1]).transpose(0, 1).reshape(N, t.shape[1]).contiguous()
 
     return perm(Wq), perm(S)
+
+
+def _calibration_hessians(hf_model, calib_ids: torch.Tensor) -> dict:
+    """Run the HF model on calib_ids and return {(layer, stack): H} with H = 2 X^T X / T
+    (float64, on the model's device) of the inputs X of each stack of linear layers that share
+    an input (wqkv: q/k/v_proj, wo: o_proj, wgu: gate/up_proj, wd: down_proj)."""
+    ids = calib_ids if calib_ids.ndim == 2 else calib_ids[None]
+    sums: dict = {}
+    hooks = []
+
+    def hook(key):
+        def fn(_mod, args):
+            x = args[0].detach().reshape(-1, args[0].shape[-1]).to(torch.float64)
+            s, n = sums.get(key, (0.0, 0))
+            sums[key] = (s + x.t() @ x, n + x.shape[0])
+        return fn
+
+    for li, layer in enumerate(hf_model.model.layers):
+        for name, mod in (("wqkv", layer.self_attn.q_proj), ("wo", layer.self_attn.o_proj),
+                          ("wgu", layer.mlp.gate_proj), ("wd", layer.mlp.down_proj)):
+            hooks.append(mod.register_forward_pre_hook(hook((li, name))))
+    try:
+        with torch.no_grad():
+            hf_model(ids.to(next(hf_model.parameters()).device))
+    finally:
+        for h in hooks:
+            h.remove()
+    return {key: (2.0 / n) * s for key, (s, n) in sums.items()}
 
 
 class Qwen2Runner:
@@ -160,9 +189,17 @@ class Qwen2Runner:
 
     @classmethod
     def from_hf(cls, hf_model, device="cuda", group: int = 128,
-                kernels: Kernels | None = None) -> "Qwen2Runner":
+                kernels: Kernels | None = None, calib_ids: torch.Tensor | None = None,
+                damp: float = 0.01) -> "Qwen2Runner":
         """Quantize a Hugging Face Qwen2ForCausalLM's weights (as the reference's
-        Qwen2Runner.__init__ + quantize, qwen.py:43-99; default, unscaled RoPE only)."""
+        Qwen2Runner.__init__ + quantize, qwen.py:43-99; default, unscaled RoPE only).
+
+        Without ``calib_ids`` every linear layer is quantized by round to nearest, as the
+        reference does. With ``calib_ids`` (token ids [B, T] or [T]) the HF model is run once on
+        them, the inputs of every linear layer are accumulated into that layer's Hessian
+        2 X^T X / T (float64), and each layer is quantized by GPTQ (``nanoserve_amd.gptq``) into
+        the same format: the calibrated quantizer the reference names as its next step
+        (README.md:233-235). The activations come from the unquantized model."""
         cfg = hf_model.config
         k = kernels or Kernels()
         rs = getattr(cfg, "rope_scaling", None)
@@ -187,8 +224,16 @@ class Qwen2Runner:
         def bf(t):
             return t.detach().to(device=device, dtype=torch.bfloat16).contiguous()
 
+        hess = _calibration_hessians(hf_model, calib_ids) if calib_ids is not None else None
+
+        def quantize(li, name, ws):
+            W = bf(torch.cat([w.detach() for w in ws]))
+            if hess is None:
+                return k.w4_quantize(W, group)
+            return gptq.quantize_layer(k, W, H=hess[(li, name)], group=group, damp=damp)
+
         layers = []
-        for layer in m.layers:
+        for li, layer in enumerate(m.layers):
             at, mlp = layer.self_attn, layer.mlp
             L = {"ln_in": bf(layer.input_layernorm.weight),
                  "ln_post": bf(layer.post_attention_layernorm.weight),
@@ -199,7 +244,7 @@ class Qwen2Runner:
                       "wgu": [mlp.gate_proj.weight, mlp.up_proj.weight],
                       "wd": [mlp.down_proj.weight]}
             for name, ws in stacks.items():
-                L[name] = k.w4_quantize(bf(torch.cat([w.detach() for w in ws])), group)
+                L[name] = quantize(li, name, ws)
             L["wgu"] = interleave_gate_up(*L["wgu"])
             layers.append(L)
         return cls(shape, bf(m.embed_tokens.weight), bf(m.norm.weight),

@@ -443,6 +443,36 @@ def _check_logits(out, ref):
     assert R.logits_match(out, ref), R.logits_gap(out, ref)
 
 
+def test_runner_gptq_calibration(k):
+    """from_hf with calibration ids: the runner (GPTQ weights) still matches the HF model holding
+    its dequantized weights, and its logits are closer to the unquantized model's than the
+    round-to-nearest runner's, on the calibration tokens and on held-out tokens."""
+    V = 512
+    m = _hf_model(256, 2, 1, 512, V, layers=2, seed=3)
+    g = torch.Generator().manual_seed(0)
+    calib = torch.randint(0, V, (4, 64), generator=g)
+    held = torch.randint(0, V, (1, 48), generator=g)
+    rtn = Qwen2Runner.from_hf(m, device=DEV, kernels=k)
+    cal = Qwen2Runner.from_hf(m, device=DEV, kernels=k, calib_ids=calib)
+    with torch.no_grad():
+        dense_c = m(calib[:1]).logits[0]
+        dense_h = m(held).logits[0]
+        eff_c = _effective_hf(m, cal)(calib[:1]).logits[0]
+
+    def gap(runner, ids, dense):
+        out = runner.forward(ids[0].to(DEV), 0).float().cpu()
+        return float((out - dense).norm() / dense.norm())
+
+    out = cal.forward(calib[0].to(DEV), 0)
+    torch.cuda.synchronize()
+    _check_logits(out, eff_c)
+    g_c, r_c = gap(cal, calib[:1], dense_c), gap(rtn, calib[:1], dense_c)
+    g_h, r_h = gap(cal, held, dense_h), gap(rtn, held, dense_h)
+    print(f"logits gap to the dense model: calib gptq {g_c:.4f} rtn {r_c:.4f}; "
+          f"held-out gptq {g_h:.4f} rtn {r_h:.4f}", flush=True)
+    assert g_c < 0.6 * r_c and g_h < 0.9 * r_h
+
+
 @pytest.mark.parametrize("H,nh,nkv,I,V,T", [(896, 7, 1, 1024, 1000, 12),
                                              (256, 2, 1, 512, 512, 5),
                                              (512, 4, 2, 768, 640, 130)])
