@@ -179,8 +179,10 @@ def main():
     def decode_step(reps=40, ctx=1024):
         """config 5: one decode step of a random-init W4A16 Qwen2.5-7B (28 layers, fused QKV and
         gate+up, bf16 lm_head) at context 1024 with a bf16 KV cache filled with N(0,1); the step
-        is one HIP graph replay (ns_w4_linear x4, ns_decode_qkv, ns_decode_attention,
-        ns_rmsnorm x2, ns_swiglu per layer; embedding gather and lm_head GEMM in torch)."""
+        is one HIP graph replay: per layer ns_w4_gemv_decode (q/k/v, add + RMSNorm in),
+        ns_decode_qkv_attention, ns_w4_gemv_decode_attn (o), ns_w4_gemv_decode (gate/up, add +
+        RMSNorm in, SwiGLU out), ns_w4_gemv_decode (down); then ns_bf16_gemv (final add + RMSNorm
+        + lm_head) and torch's embedding gather."""
         from nanoserve_amd.qwen import Qwen2Runner, Qwen2Shape
 
         shape = Qwen2Shape()
@@ -261,6 +263,59 @@ def main():
             del W, X, U, Wq, S, Wr, Sr
         torch.cuda.empty_cache()
         return res
+
+    def library_reference():
+        """What vendor library kernels reach on the same box and shapes, for context: the bf16
+        GEMM (torch.matmul -> hipBLASLt; unquantized bf16 weights, so twice the weight bytes of
+        the W4 GEMM but no dequantization) at the config-4 shapes, and torch's device copy of the
+        dominant layer's byte count (rotating buffers past the MALL) as a library stream rate."""
+        ref = {}
+        for name, N, K in layers:
+            if name not in ("gate_up", "down"):
+                continue
+            wb = torch.randn(N, K, device=dev).to(torch.bfloat16)
+            for M in (512, 2048):
+                xa = torch.randn(M, K, device=dev).to(torch.bfloat16)
+                torch.matmul(xa, wb.t())
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                runs = []
+                for _ in range(3):
+                    e0.record()
+                    for _ in range(6):
+                        torch.matmul(xa, wb.t())
+                    e1.record()
+                    torch.cuda.synchronize()
+                    runs.append(e0.elapsed_time(e1) / 6)
+                ms = statistics.median(runs)
+                tf = synth.gemm_flops(M, N, K) / (ms * 1e-3) / 1e12
+                ref[f"hipblaslt_bf16_{name}_m{M}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
+                                                      "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+                del xa
+            del wb
+        nb = synth.gemv_bytes(1, 37888, 3584, G)
+        nbuf = max(2, -(-ROTATE_BYTES // (2 * nb)))
+        srcs = [torch.ones(nb // 4, dtype=torch.int32, device=dev) for _ in range(nbuf)]
+        dsts = [torch.empty_like(t) for t in srcs]
+        for a, b in zip(dsts, srcs):
+            a.copy_(b)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        runs = []
+        for _ in range(3):
+            e0.record()
+            for a, b in zip(dsts, srcs):
+                a.copy_(b)
+            e1.record()
+            torch.cuda.synchronize()
+            runs.append(e0.elapsed_time(e1) / nbuf)
+        ms = statistics.median(runs)
+        ref["torch_copy_gate_up_bytes"] = {"bytes_read": nb, "bytes_written": nb,
+                                           "us": round(ms * 1e3, 2),
+                                           "gbs_read_plus_write": round(2 * nb / (ms * 1e-3) / 1e9, 1)}
+        del srcs, dsts
+        torch.cuda.empty_cache()
+        return ref
 
     def packed_sets():
         """The same M = 1 and M = 8 sets on the packed tile format (ns_w4_repack once, then
@@ -387,6 +442,7 @@ def main():
         extra["config4_gemm"] = gemm_set()
         extra["config5_decode"] = decode_step()
         extra["gptq"] = gptq_set()
+        extra["library_reference"] = library_reference()
 
 
     # ---------------- CPU baseline (PyTorch CPU dequant + fp32 matmul), full M=1 set

@@ -81,6 +81,20 @@ int ns_w4_linear_packed(const void* X, const void* Wp, const void* Sp, void* Y, 
                         int K, int G, void* stream);
 
 /*
+ * No counterpart in the reference's C ABI: ns_w4_linear followed by ns_swiglu, the reference's
+ * MLP activation (python/nanoserve/qwen.py:159, swiglu(linear(h, "g"), linear(h, "u"))), in
+ * one launch. The rows of Wq / S are gate and up rows interleaved in blocks of 8 (rows 16b ..
+ * 16b+7 = gate rows 8b .. 8b+7, rows 16b+8 .. 16b+15 = up rows 8b .. 8b+7; N = 2 I).
+ * Y [M][N/2] bf16 = bf16(silu(g) * u), g and u the bf16 outputs ns_w4_linear would give for
+ * the gate and up rows, silu in fp32 as ns_swiglu. M == 1: the decode GEMV (G == 128,
+ * K % 128 == 0, as ns_w4_gemv_decode); M % 128 == 0: the prefill GEMM (N % 128 == 0, K % 64 == 0,
+ * G a power of two >= 32, K % G == 0). Returns -2 for any other shape, N % 16 != 0, NULL or
+ * misaligned pointers (X, Wq 16-byte aligned).
+ */
+int ns_w4_linear_swiglu(const void* X, const void* Wq, const void* S, void* Y, int M, int N,
+                        int K, int G, void* stream);
+
+/*
  * Bytes of fp32 workspace ns_w4_gptq needs for N rows (128 * N * 4); 0 for N <= 0.
  */
 size_t ns_w4_gptq_workspace(int N);

@@ -58,6 +58,22 @@ int ns_w4_linear(const void* X, const void* Wq, const void* S, void* Y, int M, i
   return last_status();
 }
 
+int ns_w4_linear_swiglu(const void* X, const void* Wq, const void* S, void* Y, int M, int N,
+                        int K, int G, void* stream) {
+  if (M <= 0 || N <= 0 || K <= 0 || G <= 0 || N % 16) return -2;
+  if (!X || !Wq || !S || !Y) return -2;
+  if (!aligned(X, 16) || !aligned(Wq, 16) || !aligned(S, 2) || !aligned(Y, 2)) return -2;
+  if (M == 1) return ns_w4_gemv_decode(X, nullptr, nullptr, nullptr, 0.f, nullptr, Wq, S, Y, N, K,
+                                       G, 1, stream);
+  if (M % 128 || N % 128 || K % 32 || G % 32 || K % G || !ns::gemm_v2_ok(M, N, K, G)) return -2;
+  const ns::GemmArgs a{static_cast<const uint16_t*>(X), static_cast<const uint32_t*>(Wq),
+                       static_cast<const uint16_t*>(S), static_cast<uint16_t*>(Y), M, N, K, G};
+  const hipError_t e = ns::launch_gemm_swiglu(a, ns::gemm_plan(M, N, K, G),
+                                              static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return static_cast<int>(e);
+  return last_status();
+}
+
 int ns_w4_gemv_decode(const void* X, const void* res, const void* r, const void* norm_w,
                       float eps, void* res_out, const void* Wq, const void* S, void* Y, int N,
                       int K, int G, int swiglu, void* stream) {

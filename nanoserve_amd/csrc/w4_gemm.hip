@@ -310,6 +310,33 @@ __device__ __forceinline__ void store_tile_direct(const f32x16_t (&acc)[MI][NJ],
     }
 }
 
+// SwiGLU epilogue (weights' rows are gate and up rows interleaved in blocks of 8: columns 16b ..
+// 16b+7 of the product are gate rows 8b .., columns 16b+8 .. 16b+15 the matching up rows).
+// Column pairs (n, n + 8) sit in lanes l and l ^ 8 of a 32x32 fragment (same row), so one
+// shuffle pairs them; each product is rounded to bf16 first, as the separate GEMM and SwiGLU
+// would store it, and Y [M][N/2] gets bf16(silu(g) * u) at column 8b + n % 8.
+template <int MI, int NJ>
+__device__ __forceinline__ void store_tile_swiglu(const f32x16_t (&acc)[MI][NJ], uint16_t* Y,
+                                                  int M, int N, int m0, int n0w) {
+  const int lane = threadIdx.x & 63, ln = lane & 31, kh = lane >> 5;
+  const int Nh = N >> 1;
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int n = n0w + 32 * j + ln;
+      const int o = ((n >> 4) << 3) + (n & 7);
+      const bool gate = (ln & 8) == 0 && n < N;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
+        const float g = round_bf16(acc[i][j][r]);
+        const float u = __shfl_xor(g, 8, kWave);
+        if (gate && m < M) Y[(size_t)m * Nh + o] = (uint16_t)f32_to_bf16_rne(silu_mul(g, u));
+      }
+    }
+}
+
 // One 16-byte buffer load per lane into LDS at dst + 16 * lane. (A plain device function: the
 // builtin inside a lambda of a kernel template keeps the host pass from emitting the launch stub.)
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint16_t* dst, uint32_t voff,
@@ -334,11 +361,10 @@ __device__ __forceinline__ void wait_vmcnt_c() {
   __builtin_amdgcn_s_waitcnt(imm);
 }
 
-template <int BM, int WN, int NWN, int ST>
+template <int BM, int WN, int NWN, int ST, bool SW = false>
 __global__ __launch_bounds__(NWN * kWave) void w4_gemm2_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ Wq,
     const uint16_t* __restrict__ S, uint16_t* __restrict__ C, int M, int N, int K, int lgG) {
-  constexpr int THREADS = NWN * kWave;
   constexpr int MI = BM / 32, NJ = WN / 32, BN = WN * NWN;
   constexpr int STAGE = BM * BK;                 // bf16 elements per stage
   constexpr int IPW = BM / (8 * NWN);            // 16-byte LDS-load instructions per wave per block
@@ -486,7 +512,9 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm2_kernel(
 
   wait_vmcnt_c<0>();  // the trailing out-of-range loads have landed before the LDS is reused
   lds_barrier();      // every wave is done reading the ring
-  if constexpr (kLdsEpilogue)
+  if constexpr (SW)
+    store_tile_swiglu<MI, NJ>(acc, C, M, N, m0, n0 + wv * WN);
+  else if constexpr (kLdsEpilogue)
     store_tile_lds<MI, NJ, ELS>(acc, &As[wv * BM * ELS], C, M, N, m0, n0 + wv * WN);
   else
     store_tile_direct<MI, NJ>(acc, C, M, N, m0, n0 + wv * WN);
@@ -568,6 +596,22 @@ hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
     case 5:
       hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
                          a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gemm_swiglu(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
+  const dim3 grid((a.N + p.bn - 1) / p.bn, (a.M + p.bm - 1) / p.bm);
+  switch (p.cfg) {
+    case 4:
+      hipLaunchKernelGGL((w4_gemm2_kernel<128, 32, 4, 3, true>), grid, dim3(256), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 5:
+      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4, true>), grid, dim3(256), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     default:
       return hipErrorInvalidValue;

@@ -73,6 +73,9 @@ struct GemmPlan {
 
 GemmPlan gemm_plan(int M, int N, int K, int G);
 hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st);
+// The GEMM with the SwiGLU epilogue (a.C is Y [M][N/2]); only the plans gemm_v2_ok admits.
+bool gemm_v2_ok(int M, int N, int K, int G);
+hipError_t launch_gemm_swiglu(const GemmArgs& a, const GemmPlan& p, hipStream_t st);
 
 hipError_t launch_quantize(const uint16_t* W, uint32_t* Wq, uint16_t* S, int N, int K, int G,
                            hipStream_t st);

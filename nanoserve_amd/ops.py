@@ -37,6 +37,7 @@ SIGNATURES["ns_w4_gemv_decode"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _VP, _VP,
 SIGNATURES["ns_bf16_gemv"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _I32, _I32, _VP]
 SIGNATURES["ns_w4_repack"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_w4_linear_packed"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
+SIGNATURES["ns_w4_linear_swiglu"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_w4_gptq_workspace"] = [_I32]
 SIGNATURES["ns_w4_gptq"] = [_VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32, _VP]
 RESTYPES = {"ns_decode_attention_workspace": _SZ, "ns_w4_gptq_workspace": _SZ}
@@ -95,6 +96,44 @@ class Kernels:
                                      self._stream())
         self._check(rc, "ns_w4_quantize")
         return Wq, S
+
+    def w4_linear_swiglu(self, x, Wq, S, group=128, out=None):
+        """x [M, K] bf16 -> [M, N // 2] bf16 = swiglu of x @ deq(Wq, S)^T whose rows are gate and
+        up rows interleaved in blocks of 8 (``qwen.interleave_gate_up``): one launch for M = 1
+        and M % 128 == 0 (ns_w4_linear_swiglu). Other M pad with zero rows to a multiple of 128
+        above 8, and run as ``w4_linear`` + ``swiglu`` for M = 2..8 (not in the reference,
+        whose MLP is swiglu(linear(h, "g"), linear(h, "u")), qwen.py:159)."""
+        _require_gpu_tensor(x, "x", torch.bfloat16)
+        _require_gpu_tensor(Wq, "Wq", torch.int32)
+        _require_gpu_tensor(S, "S", torch.bfloat16)
+        M, K = x.shape
+        N = Wq.shape[0]
+        if N % 16:
+            raise ValueError("the interleaved gate/up matrix needs N % 16 == 0")
+        I = N // 2
+        if out is not None:
+            _require_gpu_tensor(out, "out", torch.bfloat16)
+            if tuple(out.shape) != (M, I) or not out.is_contiguous():
+                raise ValueError(f"out must be a contiguous tensor of shape {(M, I)}")
+        if 2 <= M <= 8:
+            gu = self.w4_linear(x, Wq, S, group).view(M, I // 8, 2, 8)
+            return self.swiglu(gu[:, :, 0].reshape(M, I), gu[:, :, 1].reshape(M, I), out=out)
+        Mp = M if M == 1 else ((M + 127) // 128) * 128
+        if Mp != M:
+            x = torch.cat([x, x.new_zeros(Mp - M, K)])
+        x = x.contiguous()
+        y = out if out is not None and Mp == M else torch.empty((Mp, I), dtype=torch.bfloat16,
+                                                                 device=x.device)
+        rc = self.lib.ns_w4_linear_swiglu(x.data_ptr(), Wq.contiguous().data_ptr(),
+                                          S.contiguous().data_ptr(), y.data_ptr(), Mp, N, K,
+                                          group, self._stream())
+        self._check(rc, "ns_w4_linear_swiglu")
+        if Mp != M:
+            y = y[:M]
+            if out is not None:
+                out.copy_(y)
+                return out
+        return y
 
     def w4_gptq(self, W, U, group=128):
         """Calibrated quantization (not in the reference, whose README.md:233-235 names it as

@@ -382,7 +382,7 @@ class Qwen2Runner:
             return logits.clone()
         if (use_cache or pos0 > 0) and (self.cache_k is None or pos0 + T > self.max_len):
             raise RuntimeError("cache too small: alloc_cache(max_len) first")
-        H, I, D, G = s.hidden, s.intermediate, s.head_dim, s.group
+        D, G = s.head_dim, s.group
         qn, kn = s.heads * D, s.kv_heads * D
         x = self.embed.index_select(0, ids.to(self.dev)).contiguous()
         h = k.rmsnorm(x, None, self.layers[0]["ln_in"], s.eps)
@@ -396,8 +396,7 @@ class Qwen2Runner:
                 self._store_kv(li, kk, v, pos0)
             a = self._prompt_attention(q, kk, v, pos0, li)
             h = k.rmsnorm(x, k.w4_linear(a, *L["wo"], G), L["ln_post"], s.eps)
-            gu = k.w4_linear(h, *L["wgu"], G).view(T, I // 8, 2, 8)  # gate/up interleaved by 8
-            act = k.swiglu(gu[:, :, 0].reshape(T, I), gu[:, :, 1].reshape(T, I))
+            act = k.w4_linear_swiglu(h, *L["wgu"], G)  # gate/up rows interleaved by 8
             nxt = self.layers[li + 1]["ln_in"] if li + 1 < len(self.layers) else self.final_norm
             h = k.rmsnorm(x, k.w4_linear(act, *L["wd"], G), nxt, s.eps)
         if last_only:

@@ -37,7 +37,7 @@ def test_header_declares_the_reference_entry_points():
         "ns_rmsnorm", "ns_rope", "ns_swiglu",
         "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention",
         "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn",
-        "ns_bf16_gemv", "ns_w4_gptq_workspace", "ns_w4_gptq"])
+        "ns_bf16_gemv", "ns_w4_gptq_workspace", "ns_w4_gptq", "ns_w4_linear_swiglu"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -240,3 +240,15 @@ def test_gptq_workspace_and_rejects(k):
     assert k.lib.ns_w4_gptq(P + 8, P, P, P, P, ws, 64, 256, 128, None) == -2  # W misaligned
     assert k.lib.ns_w4_gptq(P, P + 4, P, P, P, ws, 64, 256, 128, None) == -2  # U misaligned
     assert k.lib.ns_w4_gptq(P, P, P, P, None, ws, 64, 256, 128, None) == -2
+
+
+def test_linear_swiglu_rejects(k):
+    f = k.lib.ns_w4_linear_swiglu
+    assert f(P, P, P, P, 128, 264, 256, 128, None) == -2     # N % 16
+    assert f(P, P, P, P, 4, 256, 256, 128, None) == -2       # M not 1 or a multiple of 128
+    assert f(P, P, P, P, 128, 272, 256, 128, None) == -2     # GEMM needs N % 128
+    assert f(P, P, P, P, 128, 256, 288, 32, None) == -2      # GEMM needs K % 64
+    assert f(P, P, P, P, 128, 256, 384, 96, None) == -2      # G not a power of two
+    assert f(P, P, P, P, 1, 256, 256, 64, None) == -2        # GEMV needs G == 128
+    assert f(P + 8, P, P, P, 128, 256, 256, 128, None) == -2
+    assert f(P, P, P, None, 128, 256, 256, 128, None) == -2

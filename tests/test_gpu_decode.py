@@ -315,6 +315,38 @@ def test_gemv_decode_swiglu_output(k, N, K, norm):
     close(act, ref.double().cpu(), rtol=2 ** -8, atol=1e-6)
 
 
+@pytest.mark.parametrize("M,N,K,G", [(128, 256, 256, 128), (256, 2048, 1024, 64),
+                                     (2048, 37888, 3584, 128), (128, 7168, 18944, 128),
+                                     (384, 512, 512, 32), (1, 37888, 3584, 128),
+                                     (3, 1024, 512, 128), (200, 1024, 512, 128)])
+def test_linear_swiglu_equals_linear_then_swiglu(k, M, N, K, G):
+    """ns_w4_linear_swiglu (SwiGLU in the GEMM / GEMV epilogue) against ns_w4_linear of the same
+    interleaved weights followed by ns_swiglu of the de-interleaved halves: bit for bit (the same
+    accumulation, and the products rounded to bf16 before the activation as the unfused pair
+    stores them; M = 1 to a bf16 rounding, the decode GEMV may order its fp32 sums differently);
+    M = 3 (unfused pair) and M = 200 (zero-row padding) through the wrapper."""
+    from nanoserve_amd.qwen import interleave_gate_up
+
+    print(f"linear_swiglu M={M} N={N} K={K} G={G}", flush=True)
+    W = rnd(N, K, seed=61, scale=0.02)
+    Wq, S = interleave_gate_up(*k.w4_quantize(W, G))
+    x = rnd(M, K, seed=62)
+    act = k.w4_linear_swiglu(x, Wq, S, G)
+    I = N // 2
+    g4 = k.w4_linear(x, Wq, S, G).view(M, I // 8, 2, 8)
+    ref = k.swiglu(g4[:, :, 0].reshape(M, I).contiguous(), g4[:, :, 1].reshape(M, I).contiguous())
+    torch.cuda.synchronize()
+    assert act.shape == (M, I)
+    if M == 1:  # the fused decode GEMV may split the k-groups differently: fp32 sums reordered
+        close(act, ref.double().cpu(), rtol=2 ** -8, atol=1e-6)
+    else:
+        assert torch.equal(act, ref)
+    out = torch.empty(M, I, dtype=torch.bfloat16, device=DEV)
+    assert k.w4_linear_swiglu(x, Wq, S, G, out=out) is out
+    torch.cuda.synchronize()
+    assert torch.equal(out, act)
+
+
 def test_gemv_decode_rejects(k):
     Wq, S = _w4(64, 256, seed=49)
     x = rnd(1, 256, seed=50)
