@@ -23,6 +23,8 @@
 //
 // Generic path (any K % 32 == 0, G % 32 == 0, K % G == 0): one wavefront per output row,
 // VALU fp32 FMAs with the exact fp32 dequant, cross-lane reduction.
+#include <type_traits>
+
 #include "w4_common.h"
 #include "w4_kernels.h"
 
@@ -409,7 +411,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
 //  * Branch-free inner loop: the per-chunk offsets are stored four times (one 16-byte LDS read
 //    initialises the whole MFMA accumulator), the diagonal value is picked with three selects,
 //    and lanes off the diagonal (or on a padded slot) write to a private dummy slot.
-template <int NW, int R, int GR, int XM, int YM, int XV>
+template <int NW, int R, int GR, int XM, int YM, int XV, bool FC>
 __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
     const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int N, int K, M1Fuse fz) {
@@ -628,33 +630,60 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   float* dummy = part + 2 * GR * C + lane;
   const int c_first = (16 * wv + j) % C;
   const int c_step = (16 * NW) % C;
+  // FC (the launcher checks that 16 NW is a multiple of C, e.g. gate/up: C = 28, NW = 14):
+  // every block a lane sees belongs to the same k-group, so its activation fragments and
+  // offset are read from LDS once, not per block (the same values either way).
+  f32x4_t t_fix{};
+  u32x4_t x_fix[4];
+  if constexpr (FC) {
+    t_fix = xs4[c_first];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+      x_fix[s4] = *reinterpret_cast<const u32x4_t*>(&xl[XR * c_first + 32 * kg + 8 * s4]);
+  }
   int g = blockIdx.x;
   for (int it = 0; g < ngroups; ++it, g += gstep) {
     float* pt = part + (it & 1) * GR * C + j;
     int c = c_first;
-    for (int i0 = 0; i0 < nbp; i0 += R) {
+    auto block = [&](auto fixed, int u, int b) {
+      f32x4_t t;
+      u32x4_t xf[4];
+      if constexpr (decltype(fixed)::value) {
+        t = t_fix;
 #pragma unroll
-      for (int u = 0; u < R; ++u) {
-        const int b = wv + NW * (i0 + u);
-        f32x4_t t = xs4[c];
-        const uint16_t* xr = &xl[XR * c + 32 * kg];
+        for (int s4 = 0; s4 < 4; ++s4) xf[s4] = x_fix[s4];
+      } else {
+        t = xs4[c];
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4)
-          t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              as_bf16x8(*reinterpret_cast<const u32x4_t*>(xr + 8 * s4)),
-              as_bf16x8(unpack_word_paired(ring[u][s4], vmask, sbits)), t, 0, 0, 0);
-        float v = s1 ? t[1] : t[0];
-        v = s2 ? t[2] : v;
-        v = s3 ? t[3] : v;
-        float* dst = diag && b < NBG ? pt + 16 * b : dummy;
-        *dst = bf16_bits_to_f32(rsc[u] & 0xffffu) * v;
+          xf[s4] = *reinterpret_cast<const u32x4_t*>(&xl[XR * c + 32 * kg + 8 * s4]);
+      }
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(xf[s4]), as_bf16x8(unpack_word_paired(ring[u][s4], vmask, sbits)), t, 0, 0, 0);
+      float v = s1 ? t[1] : t[0];
+      v = s2 ? t[2] : v;
+      v = s3 ? t[3] : v;
+      float* dst = diag && b < NBG ? pt + 16 * b : dummy;
+      *dst = bf16_bits_to_f32(rsc[u] & 0xffffu) * v;
+      if constexpr (!decltype(fixed)::value) {
         c += c_step;
         c = c >= C ? c - C : c;
-        __builtin_amdgcn_sched_barrier(0);
-        issue(ring[u], rsc[u]);
-        __builtin_amdgcn_sched_barrier(0);
       }
-    }
+    };
+    auto pass = [&](auto fixed) {
+      for (int i0 = 0; i0 < nbp; i0 += R) {
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+          block(fixed, u, wv + NW * (i0 + u));
+          __builtin_amdgcn_sched_barrier(0);
+          issue(ring[u], rsc[u]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    };
+    pass(std::integral_constant<bool, FC>{});
     __syncthreads();
     if (wv == it % NW) {
       const float* pr = part + (it & 1) * GR * C;
@@ -947,9 +976,9 @@ hipError_t launch_xlds(const GemvArgs& a, hipStream_t st) {
   return hipSuccess;
 }
 
-template <int NW, int R, int GR, int XM = kXPlain, int YM = kYPlain, int XV = kXVecs>
-hipError_t launch_m1(const GemvArgs& a, hipStream_t st, const M1Fuse& fz = M1Fuse{}) {
-  const void* fn = reinterpret_cast<const void*>(&w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV>);
+template <int NW, int R, int GR, int XM, int YM, int XV, bool FC>
+hipError_t launch_m1_fc(const GemvArgs& a, hipStream_t st, const M1Fuse& fz) {
+  const void* fn = reinterpret_cast<const void*>(&w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV, FC>);
   // the planner keeps the dynamic part under 96 KiB; the limit leaves room for static LDS
   static const hipError_t attr =
       hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
@@ -964,9 +993,15 @@ hipError_t launch_m1(const GemvArgs& a, hipStream_t st, const M1Fuse& fz = M1Fus
   // Two workgroups per CU: more resident waves only lengthen the memory queues.
   const int ngroups = (a.N + GR - 1) / GR;
   const int grid = max(1, min(ngroups, min(max(per_cu, 1), 2) * cus));
-  hipLaunchKernelGGL((w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV>), dim3(grid), dim3(NW * kWave), lds, st,
-                     a.X, a.Wq, a.S, a.Y, a.N, a.K, fz);
+  hipLaunchKernelGGL((w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV, FC>), dim3(grid), dim3(NW * kWave), lds,
+                     st, a.X, a.Wq, a.S, a.Y, a.N, a.K, fz);
   return hipSuccess;
+}
+
+template <int NW, int R, int GR, int XM = kXPlain, int YM = kYPlain, int XV = kXVecs>
+hipError_t launch_m1(const GemvArgs& a, hipStream_t st, const M1Fuse& fz = M1Fuse{}) {
+  if ((16 * NW) % (a.K >> 7) == 0) return launch_m1_fc<NW, R, GR, XM, YM, XV, true>(a, st, fz);
+  return launch_m1_fc<NW, R, GR, XM, YM, XV, false>(a, st, fz);
 }
 
 template <int MP, int NW, int CW, int ST, int DPW>
