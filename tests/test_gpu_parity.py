@@ -129,6 +129,19 @@ def test_gemv_every_m(kernels, oracle, M):
     check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 1e-5)
 
 
+@pytest.mark.parametrize("N,K", [(40, 128), (200, 512), (4608, 2048), (16400, 1792), (16400, 4096),
+                                 (16400, 7168), (1000, 8192), (64, 16384), (300, 2560)])
+def test_gemv_m1_kgroup_counts(kernels, oracle, N, K):
+    """M = 1 over k-group counts C = K / 128 for which the launcher does (C in 1, 4, 16, 14, 32, 56,
+    64, 128) and does not (C = 20) keep each lane's activation fragments in registers, with each
+    of the wave counts the planner picks (8, 14, 16)."""
+    G = 128
+    Wq, S = synth.weights(N, K, G, seed=N ^ K)
+    X = synth.activations(1, K, seed=K + 7)
+    y = run_linear(kernels, X, Wq, S, G)
+    check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
+
+
 @pytest.mark.parametrize("N,K,G", [(64, 96, 32), (130, 320, 64), (48, 768, 256), (32, 1152, 384),
                                    (16, 128, 128), (17, 65536 + 128, 128)])
 def test_gemv_shapes_and_groups(kernels, oracle, N, K, G):
