@@ -115,6 +115,8 @@ class Kernels:
             _require_gpu_tensor(out, "out", torch.bfloat16)
             if tuple(out.shape) != (M, I) or not out.is_contiguous():
                 raise ValueError(f"out must be a contiguous tensor of shape {(M, I)}")
+        if M == 0:
+            return out if out is not None else x.new_empty((0, I))
         if 2 <= M <= 8:
             gu = self.w4_linear(x, Wq, S, group).view(M, I // 8, 2, 8)
             return self.swiglu(gu[:, :, 0].reshape(M, I), gu[:, :, 1].reshape(M, I), out=out)
