@@ -685,7 +685,21 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     };
     pass(std::integral_constant<bool, FC>{});
     __syncthreads();
-    if (wv == it % NW) {
+    // 16-wave workgroups serve the long rows (the planner picks NW = 16 for C >= 64, e.g. down,
+    // C = 148): a wave per row, its lanes taking the row's partials c = lane, lane + 64, ...
+    // (one lane-wise pass, then a wave sum) instead of one wave walking C / 4 partials per lane
+    // for all the rows
+    constexpr bool kWideReduce = NW == 16 && YM != kYSwiglu;
+    if constexpr (kWideReduce) {
+      for (int rw = wv; rw < GR; rw += NW) {
+        const float* pr = part + (it & 1) * GR * C + rw * C;
+        float v = 0.f;
+        for (int cc = lane; cc < C; cc += kWave) v += pr[cc];
+        v = wave_sum(v);
+        const int n = GR * g + rw;
+        if (lane == 0 && n < N) Y[n] = (uint16_t)f32_to_bf16_rne(v);
+      }
+    } else if (wv == it % NW) {
       const float* pr = part + (it & 1) * GR * C;
       float v = 0.f;
       if (j < GR)
