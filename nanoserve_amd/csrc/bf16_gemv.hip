@@ -59,7 +59,8 @@ __global__ void __launch_bounds__(kLmWaves * kWave)
 #pragma unroll
     for (int b = 0; b < MAXKB; ++b) {
       const int k = 512 * b + 8 * lane;
-      dst[b] = b < KB && k < K ? *reinterpret_cast<const u32x4_t*>(base + k)
+      // read once per token: non-temporal, as the W4 weight streams
+      dst[b] = b < KB && k < K ? __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(base + k))
                                : u32x4_t{0u, 0u, 0u, 0u};
     }
   };

@@ -17,6 +17,12 @@ typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
 
 constexpr int kWave = 64;
 
+// Cache policy of the GEMV weight and scale streams (the aux operand of buffer loads: bit 0 =
+// sc0, bit 1 = nt). Each byte is read once per launch, so the loads are marked non-temporal:
+// on MI355X this made every M = 1 and M = 8 GEMV layer 3-8 % faster than default-policy loads
+// (same outputs); sc0 with nt measured on par with nt alone, slightly ahead on gate/up.
+constexpr int kStreamAux = 3;
+
 // Cache rows per split of the decode attention (decode_ops.hip); the attention-merging
 // activation load of the decode GEMV (w4_gemv.hip) reads the same split layout.
 constexpr int kAttnDecodeChunk = 256;

@@ -90,7 +90,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_mfma_kernel(
     for (int u = 0; u < UB; ++u) {
       const int c = min(cb + u, clast);
 #pragma unroll
-      for (int rt = 0; rt < RT; ++rt) wb[u][rt] = wp[rt][4 * c];
+      for (int rt = 0; rt < RT; ++rt) wb[u][rt] = __builtin_nontemporal_load(&wp[rt][4 * c]);
 #pragma unroll
       for (int s = 0; s < 4; ++s) xb[u][s] = xp[16 * c + s];
     }
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
       w[rt] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                              wres, vb + 16u * rt * rowb, so, 0));
+                                              wres, vb + 16u * rt * rowb, so, kStreamAux));
   };
   // Scales of a tile: lane (r16, h == rt) loads groups c0 .. c0 + 8 SL - 1 of row 16 rt + r16.
   auto load_scales = [&](u32x4_t (&sv)[SL], int tile) {
@@ -446,8 +446,8 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     const bool live = gr < ngroups && b < NBG;
     const uint32_t blk = (uint32_t)(gr * NBG + b);
     w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                        wres, vw, live ? 1024u * blk : kOOB, 0));
-    sc = __builtin_amdgcn_raw_buffer_load_b16(sres, vs, live ? 32u * blk : kOOB, 0);
+                                        wres, vw, live ? 1024u * blk : kOOB, kStreamAux));
+    sc = __builtin_amdgcn_raw_buffer_load_b16(sres, vs, live ? 32u * blk : kOOB, kStreamAux);
     if (++ir == nbp) {
       ir = 0;
       gr += gstep;
@@ -741,7 +741,7 @@ __device__ __forceinline__ void wait_vmcnt_lgkm0() {
 // builtin inside a lambda of a kernel template keeps the host pass from emitting the stub).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* dst, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff,
-                                           soff, 0, 0);
+                                           soff, 0, kStreamAux);
 }
 
 // LDS-staged GEMV for M = 1..8 and K <= 32 x 128 (whole rows of a 16-row group fit in LDS).

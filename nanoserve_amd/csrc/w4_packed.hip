@@ -119,8 +119,8 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_packed_kernel(
       const bool live = t < NT && g < ng;
       const uint32_t tile = (uint32_t)(t * C + wv + NW * g);
       wr[slot][g] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    wres, 16u * lane, live ? 1024u * tile : kPackOOB, 0));
-      sr[slot][g] = __builtin_amdgcn_raw_buffer_load_b16(sres, 2u * j, live ? 32u * tile : kPackOOB, 0);
+                                                    wres, 16u * lane, live ? 1024u * tile : kPackOOB, kStreamAux));
+      sr[slot][g] = __builtin_amdgcn_raw_buffer_load_b16(sres, 2u * j, live ? 32u * tile : kPackOOB, kStreamAux);
     }
   };
   const int step = gridDim.x;
@@ -211,8 +211,8 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_packed_lds_kernel(
       const bool live = t < NT && g < ng;
       const uint32_t tile = (uint32_t)(t * C + wv + NW * g);
       wr[g] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                              wres, 16u * lane, live ? 1024u * tile : kPackOOB, 0));
-      sr[g] = __builtin_amdgcn_raw_buffer_load_b16(sres, 2u * j, live ? 32u * tile : kPackOOB, 0);
+                                              wres, 16u * lane, live ? 1024u * tile : kPackOOB, kStreamAux));
+      sr[g] = __builtin_amdgcn_raw_buffer_load_b16(sres, 2u * j, live ? 32u * tile : kPackOOB, kStreamAux);
     }
   };
 
