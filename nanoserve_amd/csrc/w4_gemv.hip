@@ -911,6 +911,196 @@ size_t lds_bytes(int K, int nw, int st) {
   return (size_t)st * 16 * (64 * C + 16) + (size_t)st * 16 * C * 2 + (size_t)2 * nw * 64 * 16 + 1024;
 }
 
+// M = 2..8 streaming kernel ("half-pair" MFMA). Generalises the M = 1 kernel's diagonal trick
+// from 16 pieces of one row to 8 rows x 2 pieces: a wave instruction loads 8 rows x 128 bytes
+// (row-contiguous 128-byte runs), i.e. one 256-k "pair" (two 128-k chunks) of 8 rows.
+//  * MFMA roles (v_mfma_f32_16x16x32_bf16): B column j = (row j % 8 of the tile, half j / 8),
+//    lane (j, kq) holding words 4 kq .. 4 kq + 3 of that half-pair (step s uses word s);
+//    A row i = (activation row i % 8, half i / 8) with the matching activation k's. D[i][j] is
+//    a chunk's partial sum when the halves agree; the other half of D is discarded (the MFMA
+//    work is cheap next to the HBM stream). Rows m >= M of A are zero.
+//  * Each wave owns fixed pairs p = w, w + NW, ... (CW of them) of every row, so its
+//    activation fragments (pair order, 64 bytes per lane per pair) stay in registers for the
+//    whole kernel; the -136 * sum_k x accumulator initialisers (one MFMA against a constant
+//    operand per step) sit in a wave-private LDS table, one 16-byte read per block.
+//  * Weights as exact bf16 128 + q (paired-nibble unpack) and one fp32 scale per (row, chunk)
+//    after the four MFMAs of a block: the same exact dequant as the other GEMV kernels.
+//  * Workgroups are persistent over groups of GT 8-row tiles; a wave's CW x GT blocks of a
+//    group stream through an R-slot register ring that continues into the next group. Each
+//    wave leaves its per-tile partials (4 rows m x 1 row n per useful lane) in a double-
+//    buffered LDS table; after the group's barrier GT waves sum them over waves and halves
+//    and store Y.
+template <int CW, int GT, int R>
+__global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
+    const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
+    const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int M, int N, int K) {
+  constexpr uint32_t kOOB = 0x7fffffc0u;
+  constexpr int NB = CW * GT;  // 1 KiB blocks per wave per group
+  static_assert(NB % R == 0, "each ring slot serves fixed blocks of a group");
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int NW = blockDim.x >> 6;
+  f32x4_t* xil = reinterpret_cast<f32x4_t*>(smem);  // [NW][CW][64]
+  // partials per tile and wave: only the 32 useful lanes' (compact table, for taller groups)
+  // or all 64 lanes' (fewer registers: the compiler needs more for the compact stores)
+  constexpr bool kCompact = GT > 2;
+  constexpr int kSlots = kCompact ? 32 : kWave;
+  f32x4_t* red = xil + NW * CW * kWave;              // [2][NW][GT][kSlots]
+
+  const int P = K >> 8, C = K >> 7;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, kq = lane >> 4;
+  const int ntiles = (N + 7) >> 3;
+  const int ngroups = (ntiles + GT - 1) / GT;
+  const int gstep = gridDim.x;
+  const uint32_t RB = (uint32_t)(K >> 1);  // bytes per weight row
+
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(Wq), (short)0, (int)((size_t)N * RB), 0x00020000);
+  const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(S), (short)0, (int)((size_t)N * C * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(X), (short)0, (int)((size_t)M * K * 2), 0x00020000);
+
+  // activations first (their wait must not include the weight ring's latency): lane
+  // (i = (m, h), kq), pair t: x[m][256 p + 128 h + 32 kq .. + 31], four 16-byte loads; rows
+  // m >= M and pairs p >= P read zeros through the range check
+  const int xm = c16 & 7, xh = c16 >> 3;
+  const uint32_t vx = ((uint32_t)xm * (uint32_t)K + 128u * xh + 32u * kq) * 2u;
+  u32x4_t xa[CW][4];
+#pragma unroll
+  for (int t = 0; t < CW; ++t) {
+    const int p = wv + NW * t;
+    const uint32_t so = p < P ? 512u * (uint32_t)p : kOOB;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      xa[t][s] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xres, vx + 16u * s, so, 0));
+  }
+
+  // weight lane (j = (row nl, half hc), kq): row nl of the tile, bytes 64 hc + 16 kq of a pair
+  const int nl = c16 & 7, hc = c16 >> 3;
+  const uint32_t vw = (uint32_t)nl * RB + 64u * hc + 16u * kq;
+  const uint32_t vs = ((uint32_t)nl * (uint32_t)C + hc) * 2u;
+  auto issue = [&](u32x4_t& w, uint32_t& sc, int g, int i) {
+    const int t = i / GT, u = i % GT;
+    const int p = wv + NW * t;
+    const bool live = g < ngroups && p < P;
+    const uint32_t row0 = 8u * (uint32_t)(GT * g + u);
+    w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                        wres, vw, live ? row0 * RB + 128u * p : kOOB, kStreamAux));
+    sc = __builtin_amdgcn_raw_buffer_load_b16(
+        sres, vs, live ? (row0 * (uint32_t)C + 2u * p) * 2u : kOOB, kStreamAux);
+  };
+  u32x4_t ring[R];
+  uint32_t rsc[R];
+  int g = blockIdx.x;
+#pragma unroll
+  for (int i = 0; i < R; ++i) issue(ring[i], rsc[i], g, i);
+  __builtin_amdgcn_sched_barrier(0);
+
+  const u32x4_t kNeg136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
+  uint32_t vmask;
+  asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(vmask));
+  const uint32_t sbits = 0x43004300u;
+  // a useful lane (its half hc equals the half of its accumulator rows, kq / 2) stores its
+  // four rows m = 4 (kq % 2) + r of output row nl at slot (8 hc + nl) * 2 + kq % 2
+  const bool useful = (kq >> 1) == hc;
+  const int slot = (8 * hc + nl) * 2 + (kq & 1);
+  // With up to three pairs per wave, the first group (FIRST) converts each pair's activation fragments to pair order
+  // and computes its accumulator initialiser -136 * sum_k x (one MFMA against a constant
+  // operand per step) just before the pair's first block, so the first blocks do not wait for
+  // the activation loads of later pairs. (With four or five pairs the register budget does not
+  // allow it: the compiler then spills, so those convert everything before the first group.)
+  constexpr bool kLazy = CW <= 3;
+  auto group = [&](auto first, int it) {
+    constexpr bool FIRST = decltype(first)::value;
+    f32x4_t acc[GT];
+#pragma unroll
+    for (int u = 0; u < GT; ++u) acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int t = i / GT, u = i % GT, sl = i % R;
+      if constexpr (FIRST) {
+        if (u == 0) {
+          f32x4_t d0 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            xa[t][s] = pair_order(xa[t][s]);
+            d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[t][s]), as_bf16x8(kNeg136), d0, 0, 0, 0);
+          }
+          xil[(wv * CW + t) * kWave + lane] = d0;  // read back only by this wave
+        }
+      }
+      f32x4_t d = xil[(wv * CW + t) * kWave + lane];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(xa[t][s]), as_bf16x8(unpack_word_paired(ring[sl][s], vmask, sbits)), d, 0, 0, 0);
+      const float sc = bf16_bits_to_f32(rsc[sl] & 0xffffu);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[u][r] = __builtin_fmaf(sc, d[r], acc[u][r]);
+      __builtin_amdgcn_sched_barrier(0);
+      // refill: block i + R of this group, or of the next one
+      if (i + R < NB)
+        issue(ring[sl], rsc[sl], g, i + R);
+      else
+        issue(ring[sl], rsc[sl], g + gstep, i + R - NB);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    f32x4_t* rb = red + (size_t)(it & 1) * NW * GT * kSlots;
+    if constexpr (kCompact) {
+      if (useful) {
+#pragma unroll
+        for (int u = 0; u < GT; ++u) rb[(wv * GT + u) * kSlots + slot] = acc[u];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < GT; ++u) rb[(wv * GT + u) * kSlots + lane] = acc[u];
+    }
+    __syncthreads();
+    // output (m = lane / 8, row nl = lane % 8) of tile u: half h of every wave sits at slot
+    // (8 h + nl) * 2 + m / 4 (compact table) or lane (j = nl + 8 h, kq = 2 h + m / 4), register
+    // m % 4
+    for (int u = (wv - it % NW + NW) % NW; u < GT; u += NW) {  // every tile, also when NW < GT
+      const int om = lane >> 3, on = lane & 7;
+      const int q0 = kCompact ? 4 * (2 * on + (om >> 2)) + (om & 3)
+                              : 4 * (on + 16 * (om >> 2)) + (om & 3);
+      const int q1 = kCompact ? q0 + 4 * 16 : q0 + 4 * (8 + 32);
+      float v = 0.f;
+      for (int w = 0; w < NW; ++w) {
+        const float* pw = reinterpret_cast<const float*>(rb + (w * GT + u) * kSlots);
+        v += pw[q0] + pw[q1];
+      }
+      const int n = 8 * (GT * g + u) + on;
+      if (om < M && n < N) Y[(size_t)om * N + n] = (uint16_t)f32_to_bf16_rne(v);
+    }
+  };
+  int it = 0;
+  if constexpr (kLazy) {
+    if (g < ngroups) {
+      group(std::true_type{}, 0);
+      it = 1;
+      g += gstep;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < CW; ++t) {
+      f32x4_t d0 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        xa[t][s] = pair_order(xa[t][s]);
+        d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[t][s]), as_bf16x8(kNeg136), d0, 0, 0, 0);
+      }
+      xil[(wv * CW + t) * kWave + lane] = d0;
+    }
+  }
+  for (; g < ngroups; ++it, g += gstep) group(std::false_type{}, it);
+}
+
+size_t m8_bytes(int nw, int cw, int gt) {
+  return (size_t)nw * cw * kWave * 16 + (size_t)2 * nw * gt * (gt > 2 ? 32 : kWave) * 16;
+}
+
 // Generic fallback: one wavefront per output row, exact fp32 dequant, fp32 FMA.
 template <int MMAX>
 __global__ __launch_bounds__(256) void w4_gemv_generic_kernel(
@@ -1018,6 +1208,76 @@ hipError_t launch_m1(const GemvArgs& a, hipStream_t st, const M1Fuse& fz = M1Fus
   return launch_m1_fc<NW, R, GR, XM, YM, XV, false>(a, st, fz);
 }
 
+// Workgroups per CU the M = 2..8 kernel can hold (occupancy), or a negative error.
+template <int CW, int GT, int R>
+int m8_per_cu(int nw, hipError_t* err) {
+  const void* fn = reinterpret_cast<const void*>(&w4_gemv_m8_kernel<CW, GT, R>);
+  static const hipError_t attr =
+      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  *err = attr;
+  if (attr != hipSuccess) return 0;
+  const size_t lds = m8_bytes(nw, CW, GT);
+  if (lds > 160 * 1024 || nw < 1 || nw > 16) {
+    *err = hipErrorInvalidValue;
+    return 0;
+  }
+  int per_cu = 0;
+  *err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, nw * kWave, lds);
+  return max(per_cu, 1);
+}
+
+template <int CW, int GT, int R>
+hipError_t launch_m8(const GemvArgs& a, int nw, int cap, hipStream_t st) {
+  hipError_t e;
+  const int per_cu = m8_per_cu<CW, GT, R>(nw, &e);
+  if (e != hipSuccess) return e;
+  const size_t lds = m8_bytes(nw, CW, GT);
+  int cus = 0;
+  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+  if (e != hipSuccess) return e;
+  const int ngroups = ((a.N + 7) / 8 + GT - 1) / GT;
+  const int grid = max(1, min(ngroups, min(max(per_cu, 1), cap) * cus));
+  hipLaunchKernelGGL((w4_gemv_m8_kernel<CW, GT, R>), dim3(grid), dim3(nw * kWave), lds, st, a.X,
+                     a.Wq, a.S, a.Y, a.M, a.N, a.K);
+  return hipSuccess;
+}
+
+// Tile-group height and workgroups per CU for the M = 2..8 kernel with one or two pairs per
+// wave, from a per-CU byte count: every workgroup reads the whole activation (M K bf16, from
+// L2) once and its groups' weights, and the busiest CU sets the time. Ties go to the taller
+// group (fewer group barriers), then to fewer workgroups per CU. On MI355X at M = 8 this picks
+// 32-row groups for qkv (4608 x 3584) and gate/up (37888 x 3584, one workgroup per CU) and
+// 16-row groups for o (3584 x 3584), each the fastest of the candidates measured.
+template <int CW>
+hipError_t launch_m8_auto(const GemvArgs& a, int nw, hipStream_t st) {
+  int cus = 0;
+  hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+  if (e != hipSuccess) return e;
+  const int pc2 = m8_per_cu<CW, 2, 2>(nw, &e);
+  if (e != hipSuccess) return e;
+  const int pc4 = m8_per_cu<CW, 4, 4>(nw, &e);
+  if (e != hipSuccess) return e;
+  const double xb = 2.0 * a.M * a.K, rowb = 0.5 * a.K;
+  const int ntiles = (a.N + 7) / 8;
+  double best = 0;
+  int bgt = 2, bcap = 1;
+  for (int gt = 4; gt >= 2; gt -= 2) {
+    for (int cap = 1; cap <= min(2, gt == 4 ? pc4 : pc2); ++cap) {
+      const int groups = (ntiles + gt - 1) / gt;
+      const int wgs = min(groups, cap * cus);
+      const int gpw = (groups + wgs - 1) / wgs, wpc = (wgs + cus - 1) / cus;
+      const double cost = wpc * (xb + gpw * gt * 8 * rowb);
+      if (best == 0 || cost < 0.98 * best) {
+        best = cost;
+        bgt = gt;
+        bcap = cap;
+      }
+    }
+  }
+  if (bgt == 4) return launch_m8<CW, 4, 4>(a, nw, bcap, st);
+  return launch_m8<CW, 2, 2>(a, nw, bcap, st);
+}
+
 template <int MP, int NW, int CW, int ST, int DPW>
 hipError_t launch_lds(const GemvArgs& a, hipStream_t st, int grid_cap) {
   const void* fn = reinterpret_cast<const void*>(&w4_gemv_lds_kernel<MP, NW, CW, ST, DPW>);
@@ -1072,6 +1332,17 @@ GemvPlan gemv_plan(int M, int N, int K, int G) {
     p.gr = p.nw == 8 && groups16 > 256 && groups16 < 512 && (K / 128) % 2 == 0 ? 8 : 16;
     return p;
   }
+  // M = 2..8, K a multiple of 256 up to 20480: the half-pair streaming kernel, each wave
+  // holding up to five pairs of activation fragments in registers.
+  const int P = K / 256;
+  const int cw = (P + 15) / 16;
+  p.m8 = M >= 2 && G == 128 && K % 256 == 0 && cw <= 5 && small_buf &&
+         (size_t)M * K * 2 < ((size_t)1 << 31);
+  if (p.m8) {
+    p.rt = cw;
+    p.nw = (P + cw - 1) / cw;
+    return p;
+  }
   // M = 2..8 with whole rows of a 16-row group in LDS (K <= 4096): weights staged in LDS.
   p.lds = M >= 2 && G == 128 && C <= 32 && small_buf;
   if (p.lds) {
@@ -1107,6 +1378,16 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
     if (p.nw == 8 && p.rt == 2 && p.gr == 16) return launch_m1<8, 2, 16>(a, st);
     if (p.nw == 8 && p.rt == 2 && p.gr == 8) return launch_m1<8, 2, 8>(a, st);
     return hipErrorInvalidValue;
+  }
+  if (p.m8) {
+    switch (p.rt) {
+      case 1: return launch_m8_auto<1>(a, p.nw, st);
+      case 2: return launch_m8_auto<2>(a, p.nw, st);
+      case 3: return launch_m8<3, 2, 2>(a, p.nw, 2, st);
+      case 4: return launch_m8<4, 2, 2>(a, p.nw, 2, st);
+      case 5: return launch_m8<5, 2, 2>(a, p.nw, 2, st);
+      default: return hipErrorInvalidValue;
+    }
   }
   if (p.lds) {
     // copies per wave per group: 16 rows x ceil(C / 16) row pieces + the scale slab

@@ -142,6 +142,20 @@ def test_gemv_m1_kgroup_counts(kernels, oracle, N, K):
     check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
 
 
+@pytest.mark.parametrize("M", [2, 5, 8])
+@pytest.mark.parametrize("N,K", [(24, 256), (200, 4096), (136, 4352), (72, 12288), (40, 16384),
+                                 (24, 18944), (9, 20480)])
+def test_gemv_small_batch_pair_counts(kernels, oracle, M, N, K):
+    """M = 2..8 over 256-k pair counts P = K / 256 that give each of the activation register
+    set sizes (1..5 pairs per wave) and wave counts (1, 9, 15, 16) of the half-pair kernel, with
+    N tails inside an 8-row tile and inside a two-tile group."""
+    G = 128
+    Wq, S = synth.weights(N, K, G, seed=N + 3 * K + M)
+    X = synth.activations(M, K, seed=K + M, per_row_seed=True)
+    y = run_linear(kernels, X, Wq, S, G)
+    check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
+
+
 @pytest.mark.parametrize("N,K,G", [(64, 96, 32), (130, 320, 64), (48, 768, 256), (32, 1152, 384),
                                    (16, 128, 128), (17, 65536 + 128, 128)])
 def test_gemv_shapes_and_groups(kernels, oracle, N, K, G):
