@@ -911,6 +911,31 @@ size_t lds_bytes(int K, int nw, int st) {
   return (size_t)st * 16 * (64 * C + 16) + (size_t)st * 16 * C * 2 + (size_t)2 * nw * 64 * 16 + 1024;
 }
 
+// 4 x 4 transpose over the lane rows (row r = lanes 16 r .. 16 r + 15) and four registers: on
+// entry register j of a lane in row r holds element (r, j) of the transposed layout's
+// (j, r), i.e. afterwards register s of row r holds what register r of row s held. Two
+// stages of gfx950 lane swaps per dword: v_permlane32_swap exchanges the upper half-wave of
+// its first operand with the lower half-wave of its second (rows 2, 3 <-> 0, 1),
+// v_permlane16_swap the odd rows of its first operand with the even rows of its second.
+__device__ __forceinline__ void xpose_rows(u32x4_t (&r)[4]) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const auto v = __builtin_amdgcn_permlane32_swap(r[c][w], r[c + 2][w], false, false);
+      r[c][w] = v[0];
+      r[c + 2][w] = v[1];
+    }
+#pragma unroll
+  for (int c = 0; c < 4; c += 2)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const auto v = __builtin_amdgcn_permlane16_swap(r[c][w], r[c + 1][w], false, false);
+      r[c][w] = v[0];
+      r[c + 1][w] = v[1];
+    }
+}
+
 // M = 2..8 streaming kernel ("half-pair" MFMA). Generalises the M = 1 kernel's diagonal trick
 // from 16 pieces of one row to 8 rows x 2 pieces: a wave instruction loads 8 rows x 128 bytes
 // (row-contiguous 128-byte runs), i.e. one 256-k "pair" (two 128-k chunks) of 8 rows.
@@ -962,11 +987,14 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
   const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(X), (short)0, (int)((size_t)M * K * 2), 0x00020000);
 
-  // activations first (their wait must not include the weight ring's latency): lane
-  // (i = (m, h), kq), pair t: x[m][256 p + 128 h + 32 kq .. + 31], four 16-byte loads; rows
-  // m >= M and pairs p >= P read zeros through the range check
+  // activations first (their wait must not include the weight ring's latency). Lane
+  // (i = (m, h), kq) needs, for step s of pair t, the 16-byte piece 4 kq + s of
+  // x[m][256 p + 128 h .. + 127]; it loads piece 4 s + kq instead (so the four lanes of a row
+  // read 64 contiguous bytes per instruction, not four pieces 64 bytes apart) and a 4 x 4
+  // transpose across the lane rows (xpose_rows) puts them in place. Rows m >= M and pairs
+  // p >= P read zeros through the range check.
   const int xm = c16 & 7, xh = c16 >> 3;
-  const uint32_t vx = ((uint32_t)xm * (uint32_t)K + 128u * xh + 32u * kq) * 2u;
+  const uint32_t vx = ((uint32_t)xm * (uint32_t)K + 128u * xh) * 2u + 16u * kq;
   u32x4_t xa[CW][4];
 #pragma unroll
   for (int t = 0; t < CW; ++t) {
@@ -974,7 +1002,7 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
     const uint32_t so = p < P ? 512u * (uint32_t)p : kOOB;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      xa[t][s] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xres, vx + 16u * s, so, 0));
+      xa[t][s] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xres, vx + 64u * s, so, 0));
   }
 
   // weight lane (j = (row nl, half hc), kq): row nl of the tile, bytes 64 hc + 16 kq of a pair
@@ -1023,6 +1051,7 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
       if constexpr (FIRST) {
         if (u == 0) {
           f32x4_t d0 = {0.f, 0.f, 0.f, 0.f};
+          xpose_rows(xa[t]);
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
             xa[t][s] = pair_order(xa[t][s]);
@@ -1086,6 +1115,7 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
 #pragma unroll
     for (int t = 0; t < CW; ++t) {
       f32x4_t d0 = {0.f, 0.f, 0.f, 0.f};
+      xpose_rows(xa[t]);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         xa[t][s] = pair_order(xa[t][s]);
