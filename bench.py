@@ -66,6 +66,8 @@ def parse():
                    help="only the dominant-kernel launches (gate_up, M=1), e.g. under a profiler")
     p.add_argument("--gemm-only", action="store_true",
                    help="only the prefill GEMM launches (config 4), e.g. under a profiler")
+    p.add_argument("--m8-only", action="store_true",
+                   help="only the config-3 set (the four layers at M=8), e.g. under a profiler")
     p.add_argument("--decode-only", action="store_true",
                    help="only the config-5 decode step (28-layer W4 Qwen2.5-7B, context 1024)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -360,6 +362,18 @@ def main():
         print(json.dumps({"config5_decode": decode_step()}), flush=True)
         return
 
+    def m8_set():
+        g8 = graph_of(lambda i: step(x8, i), 4 * copies)
+        time_graph(g8)
+        ms8 = statistics.median(time_graph(g8) for _ in range(3)) / (4 * copies)
+        bytes_m8 = sum(synth.gemv_bytes(8, N, K, G) for _, N, K in layers)
+        return {"gbs": round(bytes_m8 / (ms8 * 1e-3) / 1e9, 1), "us_per_step": round(ms8 * 1e3, 3),
+                "frac_hbm": round(bytes_m8 / (ms8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    if args.m8_only:
+        print(json.dumps({"config3_m8_set": m8_set(), "launches": 4 * (4 * copies) * 4 + 4}), flush=True)
+        return
+
     bytes_m1 = sum(synth.gemv_bytes(1, N, K, G) for _, N, K in layers)
     value = ms_step = None
     if not args.dominant_only:
@@ -404,13 +418,7 @@ def main():
                                              "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         extra["per_layer"] = per_layer
 
-        g8 = graph_of(lambda i: step(x8, i), 4 * copies)
-        time_graph(g8)
-        ms8 = statistics.median(time_graph(g8) for _ in range(3)) / (4 * copies)
-        bytes_m8 = sum(synth.gemv_bytes(8, N, K, G) for _, N, K in layers)
-        extra["config3_m8_set"] = {"gbs": round(bytes_m8 / (ms8 * 1e-3) / 1e9, 1),
-                                   "us_per_step": round(ms8 * 1e3, 3),
-                                   "frac_hbm": round(bytes_m8 / (ms8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        extra["config3_m8_set"] = m8_set()
 
         # eager launches (Python + ctypes per call), for reference only
         for i in range(10):
