@@ -156,6 +156,18 @@ def test_gemv_small_batch_pair_counts(kernels, oracle, M, N, K):
     check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
 
 
+@pytest.mark.parametrize("M,N,K", [(3, 4600, 3584), (7, 37880, 3584), (4, 3580, 3584), (6, 3577, 18944),
+                                   (8, 9000, 7168)])
+def test_gemv_small_batch_group_heights(kernels, oracle, M, N, K):
+    """M = 2..8 on the config shapes with N tails: shapes where the half-pair kernel's planner
+    picks 32-row groups (one workgroup per CU), 16-row groups, and five pairs per wave."""
+    G = 128
+    Wq, S = synth.weights(N, K, G, seed=N + M)
+    X = synth.activations(M, K, seed=K - M, per_row_seed=True)
+    y = run_linear(kernels, X, Wq, S, G)
+    check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
+
+
 @pytest.mark.parametrize("N,K,G", [(64, 96, 32), (130, 320, 64), (48, 768, 256), (32, 1152, 384),
                                    (16, 128, 128), (17, 65536 + 128, 128)])
 def test_gemv_shapes_and_groups(kernels, oracle, N, K, G):
