@@ -361,24 +361,34 @@ __device__ __forceinline__ void wait_vmcnt_c() {
   __builtin_amdgcn_s_waitcnt(imm);
 }
 
-template <int BM, int WN, int NWN, int ST, bool SW = false>
-__global__ __launch_bounds__(NWN * kWave) void w4_gemm2_kernel(
+//
+// KS > 1 (tile grids too small to fill the chip, e.g. down at M = 512): KS groups of NWN waves
+// split K inside the workgroup. Group ks computes 64-k blocks ks, ks + KS, ... into its own
+// accumulators through its own part of the LDS ring (step t loads and computes block t KS + ks
+// in every group); at the end groups 1 .. KS-1 hand their accumulators to group 0 through LDS,
+// one group per round, and group 0 adds them in group order and stores the tile.
+template <int BM, int WN, int NWN, int ST, bool SW = false, int KS = 1>
+__global__ __launch_bounds__(NWN * KS * kWave) void w4_gemm2_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ Wq,
     const uint16_t* __restrict__ S, uint16_t* __restrict__ C, int M, int N, int K, int lgG) {
   constexpr int MI = BM / 32, NJ = WN / 32, BN = WN * NWN;
-  constexpr int STAGE = BM * BK;                 // bf16 elements per stage
+  constexpr int STAGE = BM * BK;                 // bf16 elements per stage and K group
   constexpr int IPW = BM / (8 * NWN);            // 16-byte LDS-load instructions per wave per block
   static_assert(BM % (8 * NWN) == 0, "whole LDS-load instructions per wave");
   constexpr uint32_t kOOB = 0x7fffffc0u;
-  __shared__ __align__(16) uint16_t As[ST * STAGE];
-  constexpr int ELS = NWN * BM * (WN + 8) <= ST * STAGE ? WN + 8 : WN;  // epilogue row stride
-  constexpr bool kLdsEpilogue = NWN * BM * ELS <= ST * STAGE;
+  constexpr int RING = ST * KS * STAGE;                          // bf16 elements
+  constexpr int PART = KS > 1 ? NWN * kWave * MI * NJ * 16 * 2 : 0;  // one group's partials
+  __shared__ __align__(16) uint16_t As[RING > PART ? RING : PART];
+  constexpr int ELS = NWN * BM * (WN + 8) <= RING ? WN + 8 : WN;  // epilogue row stride
+  constexpr bool kLdsEpilogue = NWN * BM * ELS <= RING;
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wq = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wv = wq % NWN, ks = wq / NWN;  // column slice and K group of this wave
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int KW = K >> 3, KG = K >> lgG;
   const int KB = K / BK;
+  const int T = (KB + KS - 1) / KS;  // steps
 
   const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(A), (short)0, (int)((size_t)M * K * 2), 0x00020000);
@@ -398,7 +408,8 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm2_kernel(
   auto issue_a = [&](int stage, int kb) {
     const uint32_t so = kb < KB ? 128u * kb : kOOB;
 #pragma unroll
-    for (int t = 0; t < IPW; ++t) lds_load16(ares, &As[stage * STAGE + 512 * (wv * IPW + t)], a_voff[t], so);
+    for (int t = 0; t < IPW; ++t)
+      lds_load16(ares, &As[(stage * KS + ks) * STAGE + 512 * (wv * IPW + t)], a_voff[t], so);
   };
 
   // weight loader: lane (n = lane % 32, kh = lane / 32), 16 bytes (words 4 kh .. 4 kh + 3 of the
@@ -444,7 +455,7 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm2_kernel(
   };
 
   auto compute = [&](int stage, const WRegs& r) {
-    const uint16_t* as = &As[stage * STAGE];
+    const uint16_t* as = &As[(stage * KS + ks) * STAGE];
     float sc[NJ], ns8[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -491,19 +502,19 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm2_kernel(
 #pragma unroll
   for (int p = 0; p < ST - 1; ++p) {
     __builtin_amdgcn_sched_barrier(0);
-    issue_w(wr[p], p);
-    issue_a(p, p);
+    issue_w(wr[p], p * KS + ks);
+    issue_a(p, p * KS + ks);
     __builtin_amdgcn_sched_barrier(0);
   }
-  for (int kb0 = 0; kb0 < KB; kb0 += ST) {
+  for (int t0 = 0; t0 < T; t0 += ST) {
 #pragma unroll
     for (int u = 0; u < ST; ++u) {
-      const int kb = kb0 + u;
+      const int kb = (t0 + u) * KS + ks;
       wait_vmcnt_c<IPW * (ST - 2)>();  // this wave's activation loads of block kb have landed
       lds_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      issue_w(wr[(u + ST - 1) % ST], kb + ST - 1);
-      issue_a((u + ST - 1) % ST, kb + ST - 1);
+      issue_w(wr[(u + ST - 1) % ST], kb + (ST - 1) * KS);
+      issue_a((u + ST - 1) % ST, kb + (ST - 1) * KS);
       __builtin_amdgcn_sched_barrier(0);
       if (kb < KB) compute(u, wr[u]);
       __builtin_amdgcn_sched_barrier(0);
@@ -512,6 +523,33 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm2_kernel(
 
   wait_vmcnt_c<0>();  // the trailing out-of-range loads have landed before the LDS is reused
   lds_barrier();      // every wave is done reading the ring
+  if constexpr (KS > 1) {
+    // group g hands its accumulators to group 0 in round g (lane-major: word r * 64 + lane of
+    // the wave's slice); group 0 adds them in group order
+    float* pb = reinterpret_cast<float*>(As) + wv * (kWave * MI * NJ * 16);
+#pragma unroll 1
+    for (int g = 1; g < KS; ++g) {
+      if (ks == g) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pb[((i * NJ + j) * 16 + r) * kWave + lane] = acc[i][j][r];
+      }
+      lds_barrier();
+      if (ks == 0) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] += pb[((i * NJ + j) * 16 + r) * kWave + lane];
+      }
+      lds_barrier();
+    }
+    if (ks != 0) return;  // no barrier follows
+  }
   if constexpr (SW)
     store_tile_swiglu<MI, NJ>(acc, C, M, N, m0, n0 + wv * WN);
   else if constexpr (kLdsEpilogue)
@@ -533,6 +571,9 @@ constexpr TileCfg kCfgs[] = {
     {128, 128, 0.75f},  // 3: v1, BM 128, 4 waves x 32 cols
     {128, 128, 1.00f},  // 4: v2, BM 128, 4 waves x 32 cols, 3 stages
     {64, 128, 1.00f},   // 5: v2, BM 64, 4 waves x 32 cols, 4 stages
+    {64, 128, 1.00f},   // 6: v2, BM 64, 4 waves x 32 cols, K split over 4 wave groups, 2 stages
+    {64, 128, 1.00f},   // 7: v2, BM 64, 4 waves x 32 cols, K split over 4 wave groups, 3 stages
+    {64, 128, 1.00f},   // 8: v2, BM 64, 4 waves x 32 cols, K split over 2 wave groups, 4 stages
 };
 
 }  // namespace
@@ -551,9 +592,11 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
   (void)G;
   constexpr int kCUs = 256;
   if (gemm_v2_ok(M, N, K, G)) {
-    // 128 x 128 tiles (three workgroups per CU) unless they leave CUs idle; then 64 x 128.
+    // 128 x 128 tiles (three workgroups per CU) unless they leave CUs idle; then 64 x 128 tiles
+    // with K split over two wave groups (eight waves per workgroup; on MI355X down at M = 512:
+    // 118 us against 140 for 64 x 128 without the split and 121-125 for a four-way split).
     const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
-    const int c = tiles < kCUs ? 5 : 4;
+    const int c = tiles < kCUs ? 8 : 4;
     return GemmPlan{c, kCfgs[c].bm, kCfgs[c].bn};
   }
   int best = 0;
@@ -597,6 +640,18 @@ hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
       hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
                          a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
+    case 6:
+      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 2, false, 4>), grid, dim3(1024), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 7:
+      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 3, false, 4>), grid, dim3(1024), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 8:
+      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4, false, 2>), grid, dim3(512), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
     default:
       return hipErrorInvalidValue;
   }
@@ -611,6 +666,18 @@ hipError_t launch_gemm_swiglu(const GemmArgs& a, const GemmPlan& p, hipStream_t 
       return hipSuccess;
     case 5:
       hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4, true>), grid, dim3(256), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 6:
+      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 2, true, 4>), grid, dim3(1024), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 7:
+      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 3, true, 4>), grid, dim3(1024), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 8:
+      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4, true, 2>), grid, dim3(512), 0, st, a.A, a.Wq,
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     default:
