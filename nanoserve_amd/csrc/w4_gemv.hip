@@ -397,7 +397,8 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
 //    this is the same four MFMAs as the row-tiled kernel, but HBM sees a purely sequential
 //    stream.
 //  * The accumulator starts at -136 * sum(x over the piece's k range) (per-chunk table xs in
-//    LDS), so D[j][j] = sum x * (q - 8) exactly as in the reference dequant.
+//    LDS, filled while the activation is staged: 16-lane DPP sums, so one barrier covers both),
+//    so D[j][j] = sum x * (q - 8) as in the reference dequant.
 //  * The piece's scale is S[flat piece index] (S is [N][K / 128], i.e. one bf16 per piece in
 //    the same order): 16 consecutive bf16 per block, one 2-byte buffer load per lane.
 //  * Workgroups are persistent over GR-row groups (GR = 16, or 8: GR C pieces must fill whole
@@ -512,6 +513,27 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   for (int u = 0; u < R; ++u) issue(ring[u], rsc[u]);
   __builtin_amdgcn_sched_barrier(0);
 
+  // Staging of activation vector e (8 bf16, natural order; all lanes of the wave call it): the
+  // vector goes to xl in pair order, and the 16 lanes holding chunk e / 16 (16 consecutive lanes
+  // of one wave, as e = tid + i * NW * 64) add their sums with four row shifts (DPP); the
+  // chunk's last lane stores the MFMA accumulator initialiser -136 * sum_k x, four times.
+  auto stage = [&](int e, const u32x4_t& v) {
+    float f[8];
+    unpack8(v, f);
+    float sum = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
+    // row_shr:1, 2, 4, 8 (inclusive scan; lanes shifted in from outside the row add 0)
+    sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0x111, 0xf, 0xf, false));
+    sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0x112, 0xf, 0xf, false));
+    sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0x114, 0xf, 0xf, false));
+    sum += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sum), 0x118, 0xf, 0xf, false));
+    if (e < 16 * CP) {
+      *reinterpret_cast<u32x4_t*>(&xl[(e >> 4) * XR + 8 * (e & 15)]) = pair_order(v);
+      if ((e & 15) == 15) {
+        const float o = -136.f * sum;
+        xs4[e >> 4] = f32x4_t{o, o, o, o};
+      }
+    }
+  };
   if constexpr (XM == kXAttn) {
     // merge the splits as the attention's own merge does: rescale to the running max
     // (base-2 logits), sum, divide once
@@ -553,9 +575,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
       for (int q = 0; q < 8; ++q) acc[q] *= il;
       xv = pack8(acc);
     }
-    if (tid < 16 * CP)
-      *reinterpret_cast<u32x4_t*>(&xl[(tid >> 4) * XR + 8 * (tid & 15)]) =
-          tid < KV ? pair_order(xv) : u32x4_t{0u, 0u, 0u, 0u};
+    stage(tid, tid < KV ? xv : u32x4_t{0u, 0u, 0u, 0u});
   } else if constexpr (XM != kXPlain) {
     // x = rmsnorm(res + radd) * nw, as the fused RMSNorm kernel: residual rounded to bf16,
     // sum of squares over the row (wave sums, then the workgroup's in LDS), one bf16 rounding
@@ -587,37 +607,22 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     const float inv = rsqrtf(tot / static_cast<float>(K) + fz.eps);
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
-      const int e = tid + i * NT;
-      if (e < 16 * CP) {
-        float g[8], o[8];
-        unpack8(xw[i], g);
+      float g[8], o[8];
+      unpack8(xw[i], g);  // zeros past the row: o is zero there
 #pragma unroll
-        for (int q = 0; q < 8; ++q) o[q] = v[i][q] * inv * g[q];
-        *reinterpret_cast<u32x4_t*>(&xl[(e >> 4) * XR + 8 * (e & 15)]) = pair_order(pack8(o));
-      }
+      for (int q = 0; q < 8; ++q) o[q] = v[i][q] * inv * g[q];
+      stage(tid + i * NT, pack8(o));
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < XV; ++i) {
-      const int e = tid + i * NT;
-      if (e < 16 * CP) *reinterpret_cast<u32x4_t*>(&xl[(e >> 4) * XR + 8 * (e & 15)]) = pair_order(xa[i]);
-    }
-    // rows longer than XV vectors per thread (K > 8 XV NT): the rest, loaded here
+    for (int i = 0; i < XV; ++i) stage(tid + i * NT, xa[i]);  // zeros past the row
+    // rows longer than XV vectors per thread (K > 8 XV NT): the rest, loaded here (the loop
+    // bound is uniform across each wave: NT is a multiple of 64)
     const u32x4_t* x4 = reinterpret_cast<const u32x4_t*>(X);
-    for (int e = tid + XV * NT; e < 16 * CP; e += NT)
-      *reinterpret_cast<u32x4_t*>(&xl[(e >> 4) * XR + 8 * (e & 15)]) =
-          e < KV ? pair_order(x4[e]) : u32x4_t{0u, 0u, 0u, 0u};
-  }
-  __syncthreads();
-  const u32x4_t kNeg136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
-  for (int cg = 16 * wv; cg < CP; cg += 16 * NW) {
-    const uint16_t* xr = &xl[XR * (cg + j) + 32 * kg];
-    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4)
-      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          as_bf16x8(kNeg136), as_bf16x8(*reinterpret_cast<const u32x4_t*>(xr + 8 * s4)), d, 0, 0, 0);
-    if (kg == 0) xs4[cg + j] = f32x4_t{d[0], d[0], d[0], d[0]};
+    for (int e0 = XV * NT; e0 < 16 * CP; e0 += NT) {
+      const int e = e0 + tid;
+      stage(e, e < KV ? x4[e] : u32x4_t{0u, 0u, 0u, 0u});
+    }
   }
   __syncthreads();
 
