@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace ns {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
@@ -86,10 +88,32 @@ __device__ __forceinline__ float round_bf16(float f) {
   return bf16_bits_to_f32(f32_to_bf16_rne(f));
 }
 
+// Sum over the 64 lanes, returned to every lane. DPP row shifts build each 16-lane row's sum in
+// its last lane (inclusive scan, lanes shifted in from outside the row add 0), two row
+// broadcasts (gfx9 row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3) carry it
+// to lane 63, which is read back as a scalar: no LDS round trips, unlike lane shuffles.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+  auto dpp = [](float x, auto ctrl, auto rmask) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                 decltype(ctrl)::value,
+                                                                 decltype(rmask)::value, 0xf, false));
+  };
+  using C111 = std::integral_constant<int, 0x111>;
+  using C112 = std::integral_constant<int, 0x112>;
+  using C114 = std::integral_constant<int, 0x114>;
+  using C118 = std::integral_constant<int, 0x118>;
+  using C142 = std::integral_constant<int, 0x142>;
+  using C143 = std::integral_constant<int, 0x143>;
+  using MF = std::integral_constant<int, 0xf>;
+  using MA = std::integral_constant<int, 0xa>;
+  using MC = std::integral_constant<int, 0xc>;
+  v += dpp(v, C111{}, MF{});
+  v += dpp(v, C112{}, MF{});
+  v += dpp(v, C114{}, MF{});
+  v += dpp(v, C118{}, MF{});
+  v += dpp(v, C142{}, MA{});
+  v += dpp(v, C143{}, MC{});
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
