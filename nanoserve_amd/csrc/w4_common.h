@@ -27,7 +27,7 @@ constexpr int kStreamAux = 3;
 
 // Cache rows per split of the decode attention (decode_ops.hip); the attention-merging
 // activation load of the decode GEMV (w4_gemv.hip) reads the same split layout.
-constexpr int kAttnDecodeChunk = 256;
+constexpr int kAttnDecodeChunk = 128;
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h16) {
   return __uint_as_float(h16 << 16);

@@ -276,7 +276,7 @@ class Qwen2Runner:
 
         Per layer five kernels: the q/k/v GEMV with the residual add + input RMSNorm fused
         into its activation load, the attention (bias + RoPE + KV append + attention over
-        256-row splits of the cache), the o GEMV, which merges the attention's splits as it
+        128-row splits of the cache), the o GEMV, which merges the attention's splits as it
         loads its activation, the gate/up GEMV with the post-attention add + RMSNorm fused in
         and SwiGLU fused into its output, and the down GEMV. The residual stream alternates between two
         buffers (a fused GEMV reads one and one of its workgroups writes the other)."""

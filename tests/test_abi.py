@@ -149,7 +149,7 @@ def test_decode_qkv_rejects_bad_arguments(k):
 
 def test_decode_attention_workspace_and_rejects(k):
     ws = k.lib.ns_decode_attention_workspace(28, 4, 128, 1024)
-    assert ws == 4 * 28 * 130 * 4  # 256-row splits x heads x (D + max + sum) floats
+    assert ws == 8 * 28 * 130 * 4  # 128-row splits x heads x (D + max + sum) floats
     assert k.lib.ns_decode_attention_workspace(28, 4, 64, 1024) == 0
     assert k.lib.ns_decode_attention_workspace(28, 4, 128, 0) == 0
     assert k.lib.ns_decode_attention_workspace(28, 0, 128, 64) == 0

@@ -157,7 +157,7 @@ def test_decode_attention_peaked_and_empty(k):
 @pytest.mark.parametrize("with_bias", [True, False])
 def test_decode_qkv_attention(k, Hq, Hk, with_bias):
     """The fused launch against the oracle's bias + RoPE followed by attention over the cache
-    with the new row appended, at positions inside, at the end of and across 256-row splits, at
+    with the new row appended, at positions inside, at the end of and across 128-row splits, at
     the cache's last row, beyond it (no append, attention over the whole cache) and before row
     0 (zeros); one workspace serves every launch in turn."""
     D, max_len = 128, 600
