@@ -409,8 +409,8 @@ __global__ void __launch_bounds__(kAttnBlock)
     sr[r] = ok ? sc[r] * qscale : -INFINITY;
     m = fmaxf(m, sr[r]);
   }
-  m = fmaxf(m, __shfl_xor(m, 16, kWave));
-  m = fmaxf(m, __shfl_xor(m, 32, kWave));
+  m = fmaxf(m, lane_xor16(m));
+  m = fmaxf(m, lane_xor32(m));
   if (grp == 0) red_m[w][h] = m;
   __syncthreads();
   m = red_m[0][h];
@@ -423,8 +423,8 @@ __global__ void __launch_bounds__(kAttnBlock)
     l += p;
     if (h < RP) ps[16 * w + 4 * grp + r][h] = p;
   }
-  l += __shfl_xor(l, 16, kWave);
-  l += __shfl_xor(l, 32, kWave);
+  l += lane_xor16(l);
+  l += lane_xor32(l);
   if (grp == 0) red_l[w][h] = l;
   __syncthreads();
 

@@ -88,6 +88,25 @@ __device__ __forceinline__ float round_bf16(float f) {
   return bf16_bits_to_f32(f32_to_bf16_rne(f));
 }
 
+// The value of lane l ^ 32 and of lane l ^ 16, by the gfx950 lane-swap instructions (no LDS
+// round trip, unlike a shuffle): v_permlane32_swap of a register with itself yields its lower
+// half-wave in both halves of the first result and its upper half-wave in the second;
+// v_permlane16_swap does the same for the even / odd 16-lane rows.
+__device__ __forceinline__ float lane_xor32(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (__lane_id() & 32) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor16(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (__lane_id() & 16) ? r[0] : r[1]);
+}
+// The value of lane l ^ 8 (DPP row_ror:8 rotates each 16-lane row by 8).
+__device__ __forceinline__ float lane_xor8(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+}
+
 // Sum over the 64 lanes, returned to every lane. DPP row shifts build each 16-lane row's sum in
 // its last lane (inclusive scan, lanes shifted in from outside the row add 0), two row
 // broadcasts (gfx9 row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3) carry it

@@ -331,7 +331,7 @@ __device__ __forceinline__ void store_tile_swiglu(const f32x16_t (&acc)[MI][NJ],
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
         const float g = round_bf16(acc[i][j][r]);
-        const float u = __shfl_xor(g, 8, kWave);
+        const float u = lane_xor8(g);
         if (gate && m < M) Y[(size_t)m * Nh + o] = (uint16_t)f32_to_bf16_rne(silu_mul(g, u));
       }
     }

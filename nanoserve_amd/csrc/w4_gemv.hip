@@ -709,14 +709,14 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
       float v = 0.f;
       if (j < GR)
         for (int cc = kg; cc < C; cc += 4) v += pr[j * C + cc];
-      v += __shfl_xor(v, 16, kWave);
-      v += __shfl_xor(v, 32, kWave);
+      v += lane_xor16(v);
+      v += lane_xor32(v);
       if constexpr (YM == kYSwiglu) {
         // rows 16g..16g+7 are gate rows 8g.., rows 16g+8.. the matching up rows: the bf16
         // outputs of row j and row j + 8 give activation 8g + j
         static_assert(GR == 16, "SwiGLU output needs 16-row groups");
         const float y = round_bf16(v);
-        const float up = __shfl_xor(y, 8, kWave);
+        const float up = lane_xor8(y);
         const int n = 8 * g + j;
         if (kg == 0 && j < 8 && 16 * g + j < N) Y[n] = (uint16_t)f32_to_bf16_rne(silu_mul(y, up));
       } else {
