@@ -1045,6 +1045,8 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
   // the activation loads of later pairs. (With four or five pairs the register budget does not
   // allow it: the compiler then spills, so those convert everything before the first group.)
   constexpr bool kLazy = CW <= 3;
+  // with the lazy conversion the initialisers also stay in registers (no LDS read per block)
+  f32x4_t xir[kLazy ? CW : 1];
   auto group = [&](auto first, int it) {
     constexpr bool FIRST = decltype(first)::value;
     f32x4_t acc[GT];
@@ -1062,10 +1064,17 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
             xa[t][s] = pair_order(xa[t][s]);
             d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[t][s]), as_bf16x8(kNeg136), d0, 0, 0, 0);
           }
-          xil[(wv * CW + t) * kWave + lane] = d0;  // read back only by this wave
+          if constexpr (kLazy)
+            xir[t] = d0;
+          else
+            xil[(wv * CW + t) * kWave + lane] = d0;  // read back only by this wave
         }
       }
-      f32x4_t d = xil[(wv * CW + t) * kWave + lane];
+      f32x4_t d;
+      if constexpr (kLazy)
+        d = xir[t];
+      else
+        d = xil[(wv * CW + t) * kWave + lane];
 #pragma unroll
       for (int s = 0; s < 4; ++s)
         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
