@@ -952,7 +952,8 @@ __device__ __forceinline__ void xpose_rows(u32x4_t (&r)[4]) {
 //  * Each wave owns fixed pairs p = w, w + NW, ... (CW of them) of every row, so its
 //    activation fragments (pair order, 64 bytes per lane per pair) stay in registers for the
 //    whole kernel; the -136 * sum_k x accumulator initialisers (one MFMA against a constant
-//    operand per step) sit in a wave-private LDS table, one 16-byte read per block.
+//    operand per step) stay in registers too when a wave holds up to three pairs, else in a
+//    wave-private LDS table (one 16-byte read per block).
 //  * Weights as exact bf16 128 + q (paired-nibble unpack) and one fp32 scale per (row, chunk)
 //    after the four MFMAs of a block: the same exact dequant as the other GEMV kernels.
 //  * Workgroups are persistent over groups of GT 8-row tiles; a wave's CW x GT blocks of a
@@ -1039,11 +1040,12 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
   // four rows m = 4 (kq % 2) + r of output row nl at slot (8 hc + nl) * 2 + kq % 2
   const bool useful = (kq >> 1) == hc;
   const int slot = (8 * hc + nl) * 2 + (kq & 1);
-  // With up to three pairs per wave, the first group (FIRST) converts each pair's activation fragments to pair order
-  // and computes its accumulator initialiser -136 * sum_k x (one MFMA against a constant
-  // operand per step) just before the pair's first block, so the first blocks do not wait for
-  // the activation loads of later pairs. (With four or five pairs the register budget does not
-  // allow it: the compiler then spills, so those convert everything before the first group.)
+  // With up to three pairs per wave, the first group (FIRST) transposes each pair's activation
+  // fragments into place, converts them to pair order and computes its accumulator initialiser
+  // -136 * sum_k x (one MFMA against a constant operand per step) just before the pair's first
+  // block, so the first blocks do not wait for the activation loads of later pairs. (With four
+  // or five pairs the register budget does not allow it: the compiler then spills, so those
+  // convert everything before the first group.)
   constexpr bool kLazy = CW <= 3;
   // with the lazy conversion the initialisers also stay in registers (no LDS read per block)
   f32x4_t xir[kLazy ? CW : 1];
