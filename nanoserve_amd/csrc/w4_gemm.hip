@@ -570,10 +570,7 @@ constexpr TileCfg kCfgs[] = {
     {128, 256, 0.85f},  // 2: v1, BM 128, 4 waves x 64 cols
     {128, 128, 0.75f},  // 3: v1, BM 128, 4 waves x 32 cols
     {128, 128, 1.00f},  // 4: v2, BM 128, 4 waves x 32 cols, 3 stages
-    {64, 128, 1.00f},   // 5: v2, BM 64, 4 waves x 32 cols, 4 stages
-    {64, 128, 1.00f},   // 6: v2, BM 64, 4 waves x 32 cols, K split over 4 wave groups, 2 stages
-    {64, 128, 1.00f},   // 7: v2, BM 64, 4 waves x 32 cols, K split over 4 wave groups, 3 stages
-    {64, 128, 1.00f},   // 8: v2, BM 64, 4 waves x 32 cols, K split over 2 wave groups, 4 stages
+    {64, 128, 1.00f},   // 5: v2, BM 64, 4 waves x 32 cols, K split over 2 wave groups, 4 stages
 };
 
 }  // namespace
@@ -596,7 +593,7 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
     // with K split over two wave groups (eight waves per workgroup; on MI355X down at M = 512:
     // 118 us against 140 for 64 x 128 without the split and 121-125 for a four-way split).
     const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
-    const int c = tiles < kCUs ? 8 : 4;
+    const int c = tiles < kCUs ? 5 : 4;
     return GemmPlan{c, kCfgs[c].bm, kCfgs[c].bn};
   }
   int best = 0;
@@ -637,18 +634,6 @@ hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
                          a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     case 5:
-      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
-                         a.C, a.M, a.N, a.K, ilog2(a.G));
-      return hipSuccess;
-    case 6:
-      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 2, false, 4>), grid, dim3(1024), 0, st, a.A, a.Wq,
-                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
-      return hipSuccess;
-    case 7:
-      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 3, false, 4>), grid, dim3(1024), 0, st, a.A, a.Wq,
-                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
-      return hipSuccess;
-    case 8:
       hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4, false, 2>), grid, dim3(512), 0, st, a.A, a.Wq,
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
@@ -665,18 +650,6 @@ hipError_t launch_gemm_swiglu(const GemmArgs& a, const GemmPlan& p, hipStream_t 
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     case 5:
-      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4, true>), grid, dim3(256), 0, st, a.A, a.Wq,
-                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
-      return hipSuccess;
-    case 6:
-      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 2, true, 4>), grid, dim3(1024), 0, st, a.A, a.Wq,
-                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
-      return hipSuccess;
-    case 7:
-      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 3, true, 4>), grid, dim3(1024), 0, st, a.A, a.Wq,
-                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
-      return hipSuccess;
-    case 8:
       hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4, true, 2>), grid, dim3(512), 0, st, a.A, a.Wq,
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
