@@ -16,7 +16,8 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnanoserve_amd.so")
 
 # Exported symbols and their ctypes signatures (include/nanoserve_w4.h,
-# include/nanoserve_decode.h); every function returns int except where RESTYPES says otherwise.
+# include/nanoserve_decode.h, include/nanoserve_probe.h); every function returns int except
+# where RESTYPES says otherwise.
 _VP, _I32, _I64, _F32, _SZ = (ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_float,
                               ctypes.c_size_t)
 SIGNATURES = {
@@ -40,6 +41,8 @@ SIGNATURES["ns_w4_linear_packed"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32,
 SIGNATURES["ns_w4_linear_swiglu"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_w4_gptq_workspace"] = [_I32]
 SIGNATURES["ns_w4_gptq"] = [_VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32, _VP]
+SIGNATURES["ns_probe_read"] = [_VP, _SZ, _VP, _I32, _I32, _I32, _VP]
+SIGNATURES["ns_probe_empty"] = [_I32, _I32, _VP]
 RESTYPES = {"ns_decode_attention_workspace": _SZ, "ns_w4_gptq_workspace": _SZ}
 
 
@@ -422,3 +425,15 @@ class Kernels:
                                           out.data_ptr(), M, N, K, group, self._stream())
         self._check(rc, "ns_w4_linear_packed")
         return out
+
+    # ------------------------------------------------------------------ measurement kernels
+    def probe_read(self, buf, grid, waves, depth, sink):
+        """Read-only stream over the bytes of ``buf`` (a 16-byte aligned GPU tensor) with the W4
+        GEMV's access pattern (include/nanoserve_probe.h); ``sink`` a GPU int32 tensor."""
+        rc = self.lib.ns_probe_read(buf.data_ptr(), buf.numel() * buf.element_size(),
+                                    sink.data_ptr(), grid, waves, depth, self._stream())
+        self._check(rc, "ns_probe_read")
+
+    def probe_empty(self, grid=1, threads=64):
+        """Launch an empty kernel (the per-launch floor of a graph of kernels)."""
+        self._check(self.lib.ns_probe_empty(grid, threads, self._stream()), "ns_probe_empty")

@@ -13,7 +13,8 @@ from nanoserve_amd import LIB_PATH, Kernels
 from nanoserve_amd.ops import SIGNATURES
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", h) for h in ("nanoserve_w4.h", "nanoserve_decode.h")]
+HEADERS = [os.path.join(ROOT, "include", h)
+           for h in ("nanoserve_w4.h", "nanoserve_decode.h", "nanoserve_probe.h")]
 
 
 def declared_symbols():
@@ -37,7 +38,8 @@ def test_header_declares_the_reference_entry_points():
         "ns_rmsnorm", "ns_rope", "ns_swiglu",
         "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention",
         "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn",
-        "ns_bf16_gemv", "ns_w4_gptq_workspace", "ns_w4_gptq", "ns_w4_linear_swiglu"])
+        "ns_bf16_gemv", "ns_w4_gptq_workspace", "ns_w4_gptq", "ns_w4_linear_swiglu",
+        "ns_probe_read", "ns_probe_empty"])
 
 
 def test_library_exports_every_declared_symbol():
