@@ -88,6 +88,21 @@ int ns_decode_attention(const void* q, const void* k_cache, const void* v_cache,
                         int max_len, void* stream);
 
 /*
+ * No counterpart in the reference: ns_decode_attention for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments without the workspace, same outputs bit for bit: the per-split partials go to
+ * a 4 MiB scratch array that the library holds in each GPU's memory until the process ends. The
+ * call allocates and frees nothing. Calls on one GPU share that GPU's scratch: calls that may
+ * overlap in time on one GPU (other streams, other host threads) race and must not be issued.
+ * Returns -2 where ns_decode_attention does and also when its workspace for these sizes,
+ * ns_decode_attention_workspace(Hq, Hk, D, max_len), exceeds 4 MiB (4194304 bytes; at Hq = 28
+ * that is max_len <= 36864); a hipError_t if the scratch address cannot be obtained.
+ */
+int ns_decode_attention_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                const int* pos, void* out, int Hq, int Hk, int D, int max_len,
+                                void* stream);
+
+/*
  * No counterpart in the reference's C ABI (its runner does these steps with PyTorch ops,
  * python/nanoserve/qwen.py:119-133, 147-151). ns_decode_qkv followed by ns_decode_attention in
  * one launch, without modifying qkv: the q heads get bias + RoPE at position *pos, the new k

@@ -10,6 +10,9 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "../../include/nanoserve_decode.h"
 #include "w4_common.h"
 
@@ -583,9 +586,14 @@ size_t attn_workspace(int Hq, int Hk, int D, int max_len) {
   return attn_splits(max_len) * static_cast<size_t>(Hq) * (D + 2) * sizeof(float);
 }
 
-int attn_check(int Hq, int Hk, int D, int max_len, size_t work_bytes, const void* work) {
+int attn_shape_check(int Hq, int Hk, int D, int max_len) {
   if (D != kHeadDim || Hq <= 0 || Hk <= 0 || Hq % Hk || Hq / Hk > 8 || max_len <= 0) return -2;
   if (attn_splits(max_len) > 65535) return -2;
+  return 0;
+}
+
+int attn_check(int Hq, int Hk, int D, int max_len, size_t work_bytes, const void* work) {
+  if (attn_shape_check(Hq, Hk, D, max_len)) return -2;
   if (!work || !aligned(work, 16) || work_bytes < attn_workspace(Hq, Hk, D, max_len)) return -2;
   return 0;
 }
@@ -611,6 +619,47 @@ int launch_attn(const void* q, const void* bias, const void* inv_freq, void* kc,
                        static_cast<uint16_t*>(out), Hq, Hk, max_len);
   }
   return last_status();
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ allocation-free attention
+// ns_decode_attention_noalloc keeps the per-split partials, which ns_decode_attention writes to
+// its caller's workspace, in this file-scope device array instead: each GPU holds its own copy
+// from the library's load until the process ends, and every call on that GPU shares it. Nothing
+// in it has to start at zero: the attention kernel writes every partial slot that the merge
+// kernel of the same call reads. On the host, `scratch` names a stand-in, not a device
+// address, so host code never passes it to a kernel or a copy: it uses the address that
+// hipGetSymbolAddress gives for the current device, taken once per device on the entry point's
+// first call there, with that device current.
+constexpr size_t kScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> scratch_addr[kMaxDevices];
+std::mutex scratch_mu;
+
+// The current device's copy of `scratch`: 0 and its address in *out, -2 for a device index past
+// kMaxDevices, or the hipError_t of hipGetDevice / hipGetSymbolAddress.
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return -2;
+  void* p = scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    p = scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return static_cast<int>(e);
+      scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return 0;
 }
 
 }  // namespace
@@ -695,6 +744,23 @@ int ns_decode_attention(const void* q, const void* k_cache, const void* v_cache,
   if (!ns::aligned(q, 16) || !ns::aligned(k_cache, 16) || !ns::aligned(v_cache, 16) ||
       !ns::aligned(pos, 4) || !ns::aligned(out, 2))
     return -2;
+  return ns::launch_attn<false>(q, nullptr, nullptr, const_cast<void*>(k_cache),
+                                const_cast<void*>(v_cache), pos, out, work, Hq, Hk, max_len,
+                                static_cast<hipStream_t>(stream));
+}
+
+int ns_decode_attention_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                const int* pos, void* out, int Hq, int Hk, int D, int max_len,
+                                void* stream) {
+  if (ns::attn_shape_check(Hq, Hk, D, max_len)) return -2;
+  if (ns::attn_workspace(Hq, Hk, D, max_len) > ns::kScratchBytes) return -2;
+  if (!q || !k_cache || !v_cache || !pos || !out) return -2;
+  if (!ns::aligned(q, 16) || !ns::aligned(k_cache, 16) || !ns::aligned(v_cache, 16) ||
+      !ns::aligned(pos, 4) || !ns::aligned(out, 2))
+    return -2;
+  void* work = nullptr;
+  const int rc = ns::scratch_address(&work);
+  if (rc) return rc;
   return ns::launch_attn<false>(q, nullptr, nullptr, const_cast<void*>(k_cache),
                                 const_cast<void*>(v_cache), pos, out, work, Hq, Hk, max_len,
                                 static_cast<hipStream_t>(stream));

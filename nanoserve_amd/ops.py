@@ -41,6 +41,7 @@ SIGNATURES["ns_w4_linear_packed"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32,
 SIGNATURES["ns_w4_linear_swiglu"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_w4_gptq_workspace"] = [_I32]
 SIGNATURES["ns_w4_gptq"] = [_VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32, _VP]
+SIGNATURES["ns_decode_attention_noalloc"] = [_VP, _VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_probe_read"] = [_VP, _SZ, _VP, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_probe_empty"] = [_I32, _I32, _VP]
 RESTYPES = {"ns_decode_attention_workspace": _SZ, "ns_w4_gptq_workspace": _SZ}
@@ -290,6 +291,21 @@ class Kernels:
                                           work.numel(), n_heads, n_kv_heads, head_dim,
                                           k_cache.shape[-2], self._stream())
         self._check(rc, "ns_decode_attention")
+        return out
+
+    def decode_attention_noalloc(self, q, k_cache, v_cache, pos, n_heads, n_kv_heads, head_dim,
+                                 out):
+        """decode_attention without a workspace, for callers that cannot allocate: the partials
+        go to the library's per-GPU scratch (include/nanoserve_decode.h), so calls that overlap
+        on one GPU race. ``out`` [1, Hq * D] bf16 is required (nothing is allocated here)."""
+        _require_gpu_tensor(q, "q", torch.bfloat16)
+        _require_gpu_tensor(pos, "pos", torch.int32)
+        _require_gpu_tensor(out, "out", torch.bfloat16)
+        rc = self.lib.ns_decode_attention_noalloc(q.data_ptr(), k_cache.data_ptr(),
+                                                  v_cache.data_ptr(), pos.data_ptr(),
+                                                  out.data_ptr(), n_heads, n_kv_heads, head_dim,
+                                                  k_cache.shape[-2], self._stream())
+        self._check(rc, "ns_decode_attention_noalloc")
         return out
 
     def decode_qkv_attention(self, qkv, bias, inv_freq, pos, k_cache, v_cache, n_heads,

@@ -39,7 +39,7 @@ def test_header_declares_the_reference_entry_points():
         "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention",
         "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn",
         "ns_bf16_gemv", "ns_w4_gptq_workspace", "ns_w4_gptq", "ns_w4_linear_swiglu",
-        "ns_probe_read", "ns_probe_empty"])
+        "ns_probe_read", "ns_probe_empty", "ns_decode_attention_noalloc"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -177,6 +177,26 @@ def test_decode_attention_workspace_and_rejects(k):
     assert fused(qkv=None) == -2
     assert fused(qkv=P + 8) == -2
     assert fused(work=None) == -2
+
+
+def test_decode_attention_noalloc_rejects(k):
+    """The allocation-free attention takes the workspace's checks from its sizes: beyond its
+    4 MiB scratch (at Hq = 28: max_len > 36864) it returns -2, as for any other rejected shape
+    or pointer, without touching HIP."""
+    def call(Hq=28, Hk=4, D=128, L=1024, q=P, out=P):
+        return k.lib.ns_decode_attention_noalloc(q, P, P, P, out, Hq, Hk, D, L, None)
+
+    assert k.lib.ns_decode_attention_workspace(28, 4, 128, 36864) <= 4 << 20
+    assert k.lib.ns_decode_attention_workspace(28, 4, 128, 36865) > 4 << 20
+    assert call(L=36865) == -2
+    assert call(Hq=64, Hk=8, L=16129) == -2     # 127 splits x 64 heads x 130 floats > 4 MiB
+    assert call(D=64) == -2
+    assert call(Hq=27) == -2
+    assert call(Hq=36, Hk=4) == -2
+    assert call(L=0) == -2
+    assert call(q=None) == -2
+    assert call(q=P + 8) == -2
+    assert call(out=None) == -2
 
 
 def test_gemv_decode_rejects_bad_arguments(k):
