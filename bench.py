@@ -159,6 +159,72 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1)  # ms
 
+    def deq_f32(wq, s):
+        """Plain-torch fp32 dequantization on the GPU (the reference's CPU loop restated,
+        bench/bench_w4a16.cu:156-173): nibble i of word j is k = 8j + i, w = (q - 8) * s."""
+        N, KW = wq.shape
+        shifts = torch.arange(0, 32, 4, dtype=torch.int32, device=wq.device)
+        q = (wq.unsqueeze(-1) >> shifts) & 0xF
+        w = q.reshape(N, KW * 8).to(torch.float32) - 8.0
+        return (w.view(N, s.shape[1], -1) * s.float().unsqueeze(-1)).view(N, KW * 8)
+
+    def max_rel(y, ref):
+        return float((y.float() - ref).abs().max() / ref.abs().max())
+
+    def correctness_gate():
+        """Before any timing, as the reference's bench does (bench_w4a16.cu:138-204): every
+        config-2 layer at M = 1 and M = 8 and the config-4 GEMMs at M = 512 against a plain
+        torch fp32 dequant + fp32 matmul on the GPU; max |y - ref| / max |ref| <= 1e-2."""
+        errs = {}
+        for name, N, K in layers:
+            wq, s = dev_w[name][0]
+            w = deq_f32(wq, s)
+            cases = [(1, x1[name]), (8, x8[name])]
+            if name in ("gate_up", "down"):
+                cases.append((512, dev_bits(synth.activations(512, K, seed=512), torch.bfloat16)))
+            for M, x in cases:
+                y = kern.w4_linear(x, wq, s, G)
+                errs[f"{name}_m{M}"] = max_rel(y, x.float() @ w.t())
+            del w
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        return {"max_rel_err": {k: float(f"{v:.3e}") for k, v in errs.items()},
+                "tolerance": 1e-2, "pass": all(v <= 1e-2 for v in errs.values()),
+                "reference": "torch fp32 dequant + fp32 matmul on the GPU"}
+
+    def ceiling():
+        """The launch floor (an empty kernel in a graph, per launch) and the read-only stream
+        ceiling at each config-2 layer's byte count (ns_probe_read: the GEMV's 1 KiB-per-wave
+        access pattern and cache policy, rotating buffers past the MALL, best of a few grid
+        shapes). The reference reports its GEMVs against a measured copy ceiling
+        (bench_w4a16.cu:122-136); a GEMV only reads, so its ceiling is a read stream."""
+        sink = torch.zeros(4, dtype=torch.int32, device=dev)
+        ge = graph_of(lambda i: kern.probe_empty(1, 64), 64)
+        time_graph(ge)
+        floor_us = statistics.median(time_graph(ge) for _ in range(5)) / 64 * 1e3
+        out = {"launch_floor_us": round(floor_us, 3), "read": {}}
+        shapes = ((1024, 8, 1), (2048, 4, 1), (512, 16, 1), (768, 8, 1))
+        for name, N, K in layers:
+            nb = synth.gemv_bytes(1, N, K, G) // 1024 * 1024
+            nbuf = max(4, -(-ROTATE_BYTES // nb))
+            bufs = [torch.ones(nb // 4, dtype=torch.int32, device=dev) for _ in range(nbuf)]
+            best = None
+            for grid, waves, depth in shapes:
+                g = graph_of(lambda i: kern.probe_read(bufs[i % nbuf], grid, waves, depth, sink),
+                             2 * nbuf)
+                time_graph(g)
+                us = statistics.median(time_graph(g) for _ in range(3)) / (2 * nbuf) * 1e3
+                if best is None or us < best[0]:
+                    best = (us, grid, waves, depth)
+                del g
+            us, grid, waves, depth = best
+            out["read"][name] = {"bytes": nb, "us": round(us, 3), "gbs": round(nb / us / 1e3, 1),
+                                 "frac_hbm": round(nb / us / 1e3 / HBM_PEAK_GBS, 4),
+                                 "grid": grid, "waves": waves, "depth": depth}
+            del bufs
+        torch.cuda.empty_cache()
+        return out
+
     def gemm_set():
         """config 4: prefill GEMMs, gate_up and down at M = 512 and 2048"""
         gemm = {}
@@ -375,6 +441,12 @@ def main():
         return
 
     bytes_m1 = sum(synth.gemv_bytes(1, N, K, G) for _, N, K in layers)
+    gate = None if args.dominant_only else correctness_gate()
+    if gate is not None and not gate["pass"]:
+        print(json.dumps({"metric": "W4A16 GEMV HBM GB/s (% of peak) at M=1/8; prefill GEMM "
+                          "TFLOP/s (% MFMA)", "value": None, "error": "correctness gate failed",
+                          "correctness": gate}), flush=True)
+        sys.exit(1)
     value = ms_step = None
     if not args.dominant_only:
         # ---------------- headline: M=1 set, exactly args.steps steps
@@ -405,7 +477,12 @@ def main():
         return
 
     extra = {}
+    ceil = None
     if not args.no_extra:
+        ceil = ceiling()
+        extra["ceiling"] = ceil
+        roofline["ceiling_gbs"] = ceil["read"]["gate_up"]["gbs"]
+        roofline["frac_of_ceiling"] = round(achieved / ceil["read"]["gate_up"]["gbs"], 4)
         per_layer = {}
         for name, N, K in layers:
             for M, xs in ((1, x1), (8, x8)):
@@ -415,7 +492,8 @@ def main():
                 b = synth.gemv_bytes(M, N, K, G)
                 per_layer[f"{name}_m{M}"] = {"us": round(ms * 1e3, 3),
                                              "gbs": round(b / (ms * 1e-3) / 1e9, 1),
-                                             "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                                             "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                             "frac_ceiling": round(ceil["read"][name]["us"] / (ms * 1e3), 4)}
         extra["per_layer"] = per_layer
 
         extra["config3_m8_set"] = m8_set()
@@ -459,17 +537,22 @@ def main():
         from oracle.w4_oracle import torch_cpu_linear
 
         cpu_in = []
-        for name, N, K in layers:
+        for i, (name, N, K) in enumerate(layers):
             Wq, S = host_w[name]
-            cpu_in.append((torch.from_numpy(synth.activations(1, K, seed=100).view(np.int16).copy()).view(torch.bfloat16),
+            cpu_in.append((torch.from_numpy(synth.activations(1, K, seed=100 + i).view(np.int16).copy()).view(torch.bfloat16),
                            torch.from_numpy(Wq.view(np.int32).copy()),
                            torch.from_numpy(S.view(np.int16).copy()).view(torch.bfloat16)))
+        for (name, N, K), (x, _, _) in zip(layers, cpu_in):  # the same bytes as the GPU's inputs
+            assert torch.equal(x, x1[name].cpu()), name
 
         def cpu_step():
-            for x, wq, s in cpu_in:
-                torch_cpu_linear(x, wq, s, G)
+            return [torch_cpu_linear(x, wq, s, G) for x, wq, s in cpu_in]
 
-        cpu_step()  # warmup
+        cpu_out = cpu_step()  # warmup; its outputs check the GPU's on the same inputs
+        gpu_err = {}
+        for (name, N, K), ref in zip(layers, cpu_out):
+            y = kern.w4_linear(x1[name], *dev_w[name][0], G).float().cpu()
+            gpu_err[name] = float(f"{float((y - ref).abs().max() / ref.abs().max()):.3e}")
         times = []
         t_start = time.perf_counter()
         while len(times) < 5 or (time.perf_counter() - t_start < args.cpu_seconds and len(times) < 50):
@@ -492,7 +575,8 @@ def main():
                "kind": "port",
                "sample": f"full config-2 M=1 set (4 layers), median of {len(times)} runs, "
                          f"{med * 1e3:.1f} ms/step; PyTorch CPU unpack + (q-8)*s fp32 + fp32 matmul",
-               "os_cpu_count": os.cpu_count(), "cpu_model": model}
+               "os_cpu_count": os.cpu_count(), "cpu_model": model,
+               "max_rel_err": gpu_err, "pass": all(v <= 1e-2 for v in gpu_err.values())}
 
     line = {
         "metric": "W4A16 GEMV HBM GB/s (% of peak) at M=1/8; prefill GEMM TFLOP/s (% MFMA)",
@@ -513,9 +597,13 @@ def main():
                    "weight_copies": copies, "timing": "hip graph replay, hip events"},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "correctness": gate,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
+    if cpu is not None and not cpu["pass"]:
+        print("bench.py: GPU outputs differ from the CPU baseline's beyond 1e-2", file=sys.stderr)
+        sys.exit(1)
 
 
 if __name__ == "__main__":
