@@ -36,8 +36,8 @@ int ns_rmsnorm(void* x, const void* r, const void* w, void* y, int T, int H, flo
  * (negative: Hq*D / Hk*D). Token t is at position pos0 + t; for i < D/2, with
  * a = fp32(pos0 + t) * inv_freq[i] (inv_freq [D/2] fp32):
  *   x[i] <- x[i] cos a - x[i + D/2] sin a,   x[i + D/2] <- x[i + D/2] cos a + x[i] sin a.
- * Returns -1 for D % 16 != 0, T < 0, Hq < 0, Hk < 0, strides not a multiple of 8, NULL or
- * pointers not 16-byte aligned (q, k) / 4-byte aligned (inv_freq).
+ * Returns -1 for D % 16 != 0, D > 512, T < 0, Hq < 0, Hk < 0, strides not a multiple of 8,
+ * NULL or pointers not 16-byte aligned (q, k) / 4-byte aligned (inv_freq).
  */
 int ns_rope(void* q, void* k, const void* inv_freq, int T, int Hq, int Hk, int D, int pos0,
             long long q_stride, long long k_stride, void* stream);

@@ -21,109 +21,156 @@ namespace {
 
 constexpr int kBlock = 256;
 
-// ------------------------------------------------------------------ residual add + RMSNorm
-// One workgroup per row; each thread keeps up to MAXV 8-element vectors of the row in
-// registers between the sum of squares and the scaling, so x and r are read once.
-template <int MAXV>
-__global__ void __launch_bounds__(kBlock)
-    rmsnorm_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ r,
-                   const uint16_t* __restrict__ w, uint16_t* __restrict__ y, int H, float eps) {
-  __shared__ float part[kBlock / kWave];
-  const size_t row = blockIdx.x;
-  const int vecs = H >> 3;
-  u32x4_t* xr = reinterpret_cast<u32x4_t*>(x + row * H);
-  const u32x4_t* rr = r ? reinterpret_cast<const u32x4_t*>(r + row * H) : nullptr;
-  const u32x4_t* wr = reinterpret_cast<const u32x4_t*>(w);
-  u32x4_t* yr = reinterpret_cast<u32x4_t*>(y + row * H);
+// The prompt-pass operators behind the reference's ns_rmsnorm / ns_rope / ns_swiglu entry
+// points, organised for wave64 with buffer loads: the buffer's range check returns zeros past
+// the end of a row or vector and drops stores there, so no lane needs a tail branch.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bytes_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4_t ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ void st16(__amdgpu_buffer_rsrc_t r, uint32_t off, const u32x4_t& v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((__vector_size__(4 * sizeof(int)))) int, v), r, off, 0, 0);
+}
 
-  float v[MAXV][8];
-  float ss = 0.f;
+// ------------------------------------------------------------------ residual add + RMSNorm
+// One wave per row, four rows per workgroup. Lane l holds vectors l, l + 64, ... (VPL of them,
+// 8 bf16 each) of its row for the whole kernel; the sum of squares is a DPP wave sum, so there
+// is no LDS and no barrier. With r, the bf16 residual stream x + r is written back first.
+constexpr int kRowsPerBlock = 4;
+template <int VPL>
+__global__ void __launch_bounds__(64 * kRowsPerBlock)
+    rms_rows_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ r,
+                    const uint16_t* __restrict__ w, uint16_t* __restrict__ y, int T, int H,
+                    float eps) {
+  const int row = blockIdx.x * kRowsPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (row >= T) return;  // the whole wave
+  const uint32_t lane = threadIdx.x & 63, rb = 2u * (uint32_t)H;
+  const size_t base = (size_t)row * H;
+  const auto xr = bytes_rsrc(x + base, rb), wr = bytes_rsrc(w, rb), yr = bytes_rsrc(y + base, rb);
+  u32x4_t xv[VPL], gv[VPL];
 #pragma unroll
-  for (int i = 0; i < MAXV; ++i) {
-    const int idx = threadIdx.x + i * kBlock;
-    if (idx < vecs) {
-      unpack8(xr[idx], v[i]);
-      if (rr) {
-        float b[8];
-        unpack8(rr[idx], b);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[i][e] = round_bf16(v[i][e] + b[e]);
-        xr[idx] = pack8(v[i]);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(v[i][e], v[i][e], ss);
-    }
+  for (int v = 0; v < VPL; ++v) {
+    xv[v] = ld16(xr, 16u * (lane + 64u * v));
+    gv[v] = ld16(wr, 16u * (lane + 64u * v));
   }
-  ss = wave_sum(ss);
-  if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = ss;
-  __syncthreads();
-  float tot = 0.f;
+  float f[VPL][8];
+  float ss = 0.f;
+  if (r) {
+    const auto rr = bytes_rsrc(r + base, rb);
+    u32x4_t rv[VPL];
 #pragma unroll
-  for (int i = 0; i < kBlock / kWave; ++i) tot += part[i];
-  const float inv = rsqrtf(tot / static_cast<float>(H) + eps);
+    for (int v = 0; v < VPL; ++v) rv[v] = ld16(rr, 16u * (lane + 64u * v));
 #pragma unroll
-  for (int i = 0; i < MAXV; ++i) {
-    const int idx = threadIdx.x + i * kBlock;
-    if (idx < vecs) {
-      float g[8], o[8];
-      unpack8(wr[idx], g);
+    for (int v = 0; v < VPL; ++v) {
+      float a[8];
+      unpack8(xv[v], f[v]);
+      unpack8(rv[v], a);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = v[i][e] * inv * g[e];
-      yr[idx] = pack8(o);
+      for (int e = 0; e < 8; ++e) f[v][e] = round_bf16(f[v][e] + a[e]);
+      st16(xr, 16u * (lane + 64u * v), pack8(f[v]));
     }
+  } else {
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) unpack8(xv[v], f[v]);
+  }
+#pragma unroll
+  for (int v = 0; v < VPL; ++v)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(f[v][e], f[v][e], ss);
+  const float inv = rsqrtf(wave_sum(ss) / static_cast<float>(H) + eps);
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    float g[8];
+    unpack8(gv[v], g);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g[e] = f[v][e] * inv * g[e];
+    st16(yr, 16u * (lane + 64u * v), pack8(g));
   }
 }
 
 // ------------------------------------------------------------------ RoPE
-// Rotates one 16-byte chunk of the first half of a head and its partner in the second half.
-__device__ __forceinline__ void rotate8(float (&lo)[8], float (&hi)[8], const float* inv_freq,
-                                        int c, float pos) {
+// One wave per (token, block of kHeadsPerWave heads): lane p owns rotation pairs p, p + 64, ...
+// of every head of the block (elements p and p + D/2), so each pair's angle is computed once
+// per wave and serves all the block's heads; a wave instruction moves 64 consecutive bf16 of a
+// head half. All the block's loads are issued before the rotations.
+constexpr int kHeadsPerWave = 8;
+template <int PPL>
+__global__ void __launch_bounds__(256)
+    rope_heads_kernel(uint16_t* __restrict__ q, uint16_t* __restrict__ k,
+                      const float* __restrict__ inv_freq, int T, int Hq, int Hk, int D, int pos0,
+                      long long qs, long long ks) {
+  const int H = Hq + Hk, nblk = (H + kHeadsPerWave - 1) / kHeadsPerWave;
+  const long long wid = (long long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (wid >= (long long)T * nblk) return;  // the whole wave
+  const long long t = wid / nblk;
+  const int h0 = (int)(wid % nblk) * kHeadsPerWave;
+  const int lane = threadIdx.x & 63, half = D >> 1;
+  const float pos = static_cast<float>(pos0 + t);
+  float cs[PPL], sn[PPL];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float s, co;
-    sincosf(pos * inv_freq[8 * c + e], &s, &co);
-    const float x1 = lo[e], x2 = hi[e];
-    lo[e] = x1 * co - x2 * s;
-    hi[e] = x2 * co + x1 * s;
+  for (int s = 0; s < PPL; ++s) {
+    const int p = lane + 64 * s;
+    cs[s] = 1.f;
+    sn[s] = 0.f;
+    if (p < half) sincosf(pos * inv_freq[p], &sn[s], &cs[s]);
   }
-}
-
-__global__ void __launch_bounds__(kBlock)
-    rope_kernel(uint16_t* __restrict__ q, uint16_t* __restrict__ k,
-                const float* __restrict__ inv_freq, int T, int Hq, int Hk, int D, int pos0,
-                long long qs, long long ks) {
-  const int chunks = D >> 4;
-  const size_t total = (size_t)T * (Hq + Hk) * chunks;
-  for (size_t idx = blockIdx.x * (size_t)kBlock + threadIdx.x; idx < total;
-       idx += (size_t)gridDim.x * kBlock) {
-    const int c = static_cast<int>(idx % chunks);
-    const size_t rest = idx / chunks;
-    const int h = static_cast<int>(rest % (Hq + Hk));
-    const long long t = static_cast<long long>(rest / (Hq + Hk));
-    uint16_t* base = h < Hq ? q + t * qs + (long long)h * D : k + t * ks + (long long)(h - Hq) * D;
-    u32x4_t* lo_p = reinterpret_cast<u32x4_t*>(base + 8 * c);
-    u32x4_t* hi_p = reinterpret_cast<u32x4_t*>(base + D / 2 + 8 * c);
-    float lo[8], hi[8];
-    unpack8(*lo_p, lo);
-    unpack8(*hi_p, hi);
-    rotate8(lo, hi, inv_freq, c, static_cast<float>(pos0 + t));
-    *lo_p = pack8(lo);
-    *hi_p = pack8(hi);
+  uint16_t* hp[kHeadsPerWave];
+  uint32_t lo[kHeadsPerWave][PPL], hi[kHeadsPerWave][PPL];
+#pragma unroll
+  for (int i = 0; i < kHeadsPerWave; ++i) {
+    const int h = min(h0 + i, H - 1);  // heads past H repeat the last one and are not stored
+    hp[i] = h < Hq ? q + t * qs + (long long)h * D : k + t * ks + (long long)(h - Hq) * D;
+#pragma unroll
+    for (int s = 0; s < PPL; ++s) {
+      const int p = min(lane + 64 * s, half - 1);
+      lo[i][s] = hp[i][p];
+      hi[i][s] = hp[i][p + half];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kHeadsPerWave; ++i) {
+    if (h0 + i >= H) break;  // uniform over the wave
+#pragma unroll
+    for (int s = 0; s < PPL; ++s) {
+      const int p = lane + 64 * s;
+      if (p >= half) continue;
+      const float a = bf16_bits_to_f32(lo[i][s]), b = bf16_bits_to_f32(hi[i][s]);
+      hp[i][p] = (uint16_t)f32_to_bf16_rne(a * cs[s] - b * sn[s]);
+      hp[i][p + half] = (uint16_t)f32_to_bf16_rne(b * cs[s] + a * sn[s]);
+    }
   }
 }
 
 // ------------------------------------------------------------------ SwiGLU
-__global__ void __launch_bounds__(kBlock)
-    swiglu_kernel(const u32x4_t* __restrict__ gate, const u32x4_t* __restrict__ up,
-                  u32x4_t* __restrict__ out, size_t n8) {
-  for (size_t i = blockIdx.x * (size_t)kBlock + threadIdx.x; i < n8;
-       i += (size_t)gridDim.x * kBlock) {
-    float g[8], u[8];
-    unpack8(gate[i], g);
-    unpack8(up[i], u);
+// Workgroup b covers the 16-byte vectors [kSwigluSpan b, kSwigluSpan (b + 1)) of the flattened
+// tensors, two per thread, through buffers clamped to the tensor's end (no tail branch, no
+// grid-stride loop: the grid covers the tensor exactly).
+constexpr int kSwigluVecs = 2;
+constexpr int kSwigluSpan = 256 * kSwigluVecs;
+__global__ void __launch_bounds__(256)
+    swiglu_vec_kernel(const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,
+                      uint16_t* __restrict__ out, size_t n8) {
+  const size_t v0 = (size_t)blockIdx.x * kSwigluSpan;
+  const uint32_t bytes = (uint32_t)(16 * min((size_t)kSwigluSpan, n8 - v0));
+  const auto gr = bytes_rsrc(gate + 8 * v0, bytes), ur = bytes_rsrc(up + 8 * v0, bytes),
+             orr = bytes_rsrc(out + 8 * v0, bytes);
+  u32x4_t g[kSwigluVecs], u[kSwigluVecs];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) g[e] = silu_mul(g[e], u[e]);
-    out[i] = pack8(g);
+  for (int j = 0; j < kSwigluVecs; ++j) {
+    const uint32_t off = 16u * (threadIdx.x + 256u * j);
+    g[j] = ld16(gr, off);
+    u[j] = ld16(ur, off);
+  }
+#pragma unroll
+  for (int j = 0; j < kSwigluVecs; ++j) {
+    float a[8], b[8];
+    unpack8(g[j], a);
+    unpack8(u[j], b);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = silu_mul(a[e], b[e]);
+    st16(orr, 16u * (threadIdx.x + 256u * j), pack8(a));
   }
 }
 
@@ -160,7 +207,14 @@ __global__ void __launch_bounds__(kBlock)
           hi[e] = round_bf16(hi[e] + bhi[e]);
         }
       }
-      rotate8(lo, hi, inv_freq, c, static_cast<float>(pos));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {  // pair (8c + e, 8c + e + D/2) at this position's angle
+        float sn, cs;
+        sincosf(static_cast<float>(pos) * inv_freq[8 * c + e], &sn, &cs);
+        const float a = lo[e], b = hi[e];
+        lo[e] = a * cs - b * sn;
+        hi[e] = b * cs + a * sn;
+      }
       const u32x4_t plo = pack8(lo), phi = pack8(hi);
       *lo_p = plo;
       *hi_p = phi;
@@ -669,33 +723,58 @@ extern "C" {
 
 int ns_rmsnorm(void* x, const void* r, const void* w, void* y, int T, int H, float eps,
                void* stream) {
-  if (T < 0 || H <= 0 || H % 8 || H > 8 * ns::kBlock * 4) return -1;
+  if (T < 0 || H <= 0 || H % 8 || H > 8192) return -1;
   if (!x || !w || !y) return -1;
   if (!ns::aligned(x, 16) || !ns::aligned(w, 16) || !ns::aligned(y, 16) || !ns::aligned(r, 16))
     return -1;
   if (T == 0) return 0;
-  hipLaunchKernelGGL(ns::rmsnorm_kernel<4>, dim3(T), dim3(ns::kBlock), 0,
-                     static_cast<hipStream_t>(stream), static_cast<uint16_t*>(x),
-                     static_cast<const uint16_t*>(r), static_cast<const uint16_t*>(w),
-                     static_cast<uint16_t*>(y), H, eps);
+  const auto st = static_cast<hipStream_t>(stream);
+  const dim3 grid((T + ns::kRowsPerBlock - 1) / ns::kRowsPerBlock), block(64 * ns::kRowsPerBlock);
+  auto xp = static_cast<uint16_t*>(x);
+  auto rp = static_cast<const uint16_t*>(r);
+  auto wp = static_cast<const uint16_t*>(w);
+  auto yp = static_cast<uint16_t*>(y);
+  const int vpl = (H / 8 + 63) / 64;  // 16-byte vectors per lane: 1 .. 16
+  if (vpl <= 1)
+    hipLaunchKernelGGL(ns::rms_rows_kernel<1>, grid, block, 0, st, xp, rp, wp, yp, T, H, eps);
+  else if (vpl <= 2)
+    hipLaunchKernelGGL(ns::rms_rows_kernel<2>, grid, block, 0, st, xp, rp, wp, yp, T, H, eps);
+  else if (vpl <= 4)
+    hipLaunchKernelGGL(ns::rms_rows_kernel<4>, grid, block, 0, st, xp, rp, wp, yp, T, H, eps);
+  else if (vpl <= 8)
+    hipLaunchKernelGGL(ns::rms_rows_kernel<8>, grid, block, 0, st, xp, rp, wp, yp, T, H, eps);
+  else
+    hipLaunchKernelGGL(ns::rms_rows_kernel<16>, grid, block, 0, st, xp, rp, wp, yp, T, H, eps);
   return ns::last_status();
 }
 
 int ns_rope(void* q, void* k, const void* inv_freq, int T, int Hq, int Hk, int D, int pos0,
             long long q_stride, long long k_stride, void* stream) {
-  if (T < 0 || Hq < 0 || Hk < 0 || D <= 0 || D % 16) return -1;
+  if (T < 0 || Hq < 0 || Hk < 0 || D <= 0 || D % 16 || D > 512) return -1;
   if (q_stride < 0) q_stride = static_cast<long long>(Hq) * D;
   if (k_stride < 0) k_stride = static_cast<long long>(Hk) * D;
   if (q_stride % 8 || k_stride % 8) return -1;
   if (!q || !k || !inv_freq || !ns::aligned(q, 16) || !ns::aligned(k, 16) ||
       !ns::aligned(inv_freq, 4))
     return -1;
-  const size_t total = static_cast<size_t>(T) * (Hq + Hk) * (D / 16);
-  if (total == 0) return 0;
-  hipLaunchKernelGGL(ns::rope_kernel, dim3(ns::grid_for(total)), dim3(ns::kBlock), 0,
-                     static_cast<hipStream_t>(stream), static_cast<uint16_t*>(q),
-                     static_cast<uint16_t*>(k), static_cast<const float*>(inv_freq), T, Hq, Hk,
-                     D, pos0, q_stride, k_stride);
+  const long long waves = static_cast<long long>(T) *
+                          ((Hq + Hk + ns::kHeadsPerWave - 1) / ns::kHeadsPerWave);
+  if (waves == 0) return 0;
+  if ((waves + 3) / 4 > 0x7fffffffLL) return -1;
+  const dim3 grid(static_cast<unsigned>((waves + 3) / 4)), block(256);
+  const auto st = static_cast<hipStream_t>(stream);
+  auto qp = static_cast<uint16_t*>(q);
+  auto kp = static_cast<uint16_t*>(k);
+  auto fp = static_cast<const float*>(inv_freq);
+  if (D <= 128)
+    hipLaunchKernelGGL(ns::rope_heads_kernel<1>, grid, block, 0, st, qp, kp, fp, T, Hq, Hk, D,
+                       pos0, q_stride, k_stride);
+  else if (D <= 256)
+    hipLaunchKernelGGL(ns::rope_heads_kernel<2>, grid, block, 0, st, qp, kp, fp, T, Hq, Hk, D,
+                       pos0, q_stride, k_stride);
+  else
+    hipLaunchKernelGGL(ns::rope_heads_kernel<4>, grid, block, 0, st, qp, kp, fp, T, Hq, Hk, D,
+                       pos0, q_stride, k_stride);
   return ns::last_status();
 }
 
@@ -708,9 +787,11 @@ int ns_swiglu(const void* gate, const void* up, void* out, int T, int I, void* s
       !ns::aligned(out, 16))
     return -1;
   const size_t n8 = static_cast<size_t>(n / 8);
-  hipLaunchKernelGGL(ns::swiglu_kernel, dim3(ns::grid_for(n8)), dim3(ns::kBlock), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const ns::u32x4_t*>(gate),
-                     static_cast<const ns::u32x4_t*>(up), static_cast<ns::u32x4_t*>(out), n8);
+  const size_t blocks = (n8 + ns::kSwigluSpan - 1) / ns::kSwigluSpan;
+  if (blocks > 0x7fffffffu) return -1;
+  hipLaunchKernelGGL(ns::swiglu_vec_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(gate),
+                     static_cast<const uint16_t*>(up), static_cast<uint16_t*>(out), n8);
   return ns::last_status();
 }
 
