@@ -18,6 +18,7 @@
 
 #include "../../include/nanoserve_decode.h"
 #include "w4_common.h"
+#include "w4_kernels.h"
 
 namespace ns {
 namespace {
@@ -123,8 +124,7 @@ void launch_bf16(const uint16_t* X, const uint16_t* res, const uint16_t* radd,
                  const uint16_t* nw, float eps, const uint16_t* W, uint16_t* Y, int N, int K,
                  hipStream_t st) {
   int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0) != hipSuccess || cus <= 0)
-    cus = 256;
+  if (cached_cu_count(&cus) != hipSuccess) cus = 256;  // the launch's own error is reported
   const long long blocks = (static_cast<long long>(N) + kLmWaves - 1) / kLmWaves;
   const int grid = static_cast<int>(blocks < 2LL * cus ? blocks : 2LL * cus);
   if (res)

@@ -1214,10 +1214,10 @@ hipError_t launch_xlds(const GemvArgs& a, hipStream_t st) {
   if (attr != hipSuccess) return attr;
   const size_t lds = xlds_bytes(a.M, a.K, a.G, RT, NW, R, SL);
   int per_cu = 0;
-  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NW * kWave, lds);
+  hipError_t e = cached_occupancy(fn, NW * kWave, lds, &per_cu);
   if (e != hipSuccess) return e;
   int cus = 0;
-  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+  e = cached_cu_count(&cus);
   if (e != hipSuccess) return e;
   const int ntiles = (a.N + 16 * RT - 1) / (16 * RT);
   const int grid = max(1, min(ntiles, max(per_cu, 1) * cus));
@@ -1227,7 +1227,7 @@ hipError_t launch_xlds(const GemvArgs& a, hipStream_t st) {
 }
 
 template <int NW, int R, int GR, int XM, int YM, int XV, bool FC>
-hipError_t launch_m1_fc(const GemvArgs& a, hipStream_t st, const M1Fuse& fz) {
+hipError_t launch_m1_fc(const GemvArgs& a, hipStream_t st, const M1Fuse& fz, int wpc) {
   const void* fn = reinterpret_cast<const void*>(&w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV, FC>);
   // the planner keeps the dynamic part under 96 KiB; the limit leaves room for static LDS
   static const hipError_t attr =
@@ -1235,23 +1235,24 @@ hipError_t launch_m1_fc(const GemvArgs& a, hipStream_t st, const M1Fuse& fz) {
   if (attr != hipSuccess) return attr;
   const size_t lds = m1_bytes(a.K, GR);
   int per_cu = 0;
-  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, NW * kWave, lds);
+  hipError_t e = cached_occupancy(fn, NW * kWave, lds, &per_cu);
   if (e != hipSuccess) return e;
   int cus = 0;
-  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+  e = cached_cu_count(&cus);
   if (e != hipSuccess) return e;
-  // Two workgroups per CU: more resident waves only lengthen the memory queues.
+  // wpc workgroups per CU (two unless the plan says otherwise): more resident waves only
+  // lengthen the memory queues.
   const int ngroups = (a.N + GR - 1) / GR;
-  const int grid = max(1, min(ngroups, min(max(per_cu, 1), 2) * cus));
+  const int grid = max(1, min(ngroups, min(max(per_cu, 1), wpc) * cus));
   hipLaunchKernelGGL((w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV, FC>), dim3(grid), dim3(NW * kWave), lds,
                      st, a.X, a.Wq, a.S, a.Y, a.N, a.K, fz);
   return hipSuccess;
 }
 
 template <int NW, int R, int GR, int XM = kXPlain, int YM = kYPlain, int XV = kXVecs>
-hipError_t launch_m1(const GemvArgs& a, hipStream_t st, const M1Fuse& fz = M1Fuse{}) {
-  if ((16 * NW) % (a.K >> 7) == 0) return launch_m1_fc<NW, R, GR, XM, YM, XV, true>(a, st, fz);
-  return launch_m1_fc<NW, R, GR, XM, YM, XV, false>(a, st, fz);
+hipError_t launch_m1(const GemvArgs& a, hipStream_t st, const M1Fuse& fz = M1Fuse{}, int wpc = 2) {
+  if ((16 * NW) % (a.K >> 7) == 0) return launch_m1_fc<NW, R, GR, XM, YM, XV, true>(a, st, fz, wpc);
+  return launch_m1_fc<NW, R, GR, XM, YM, XV, false>(a, st, fz, wpc);
 }
 
 // Workgroups per CU the M = 2..8 kernel can hold (occupancy), or a negative error.
@@ -1268,7 +1269,7 @@ int m8_per_cu(int nw, hipError_t* err) {
     return 0;
   }
   int per_cu = 0;
-  *err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, nw * kWave, lds);
+  *err = cached_occupancy(fn, nw * kWave, lds, &per_cu);
   return max(per_cu, 1);
 }
 
@@ -1279,7 +1280,7 @@ hipError_t launch_m8(const GemvArgs& a, int nw, int cap, hipStream_t st) {
   if (e != hipSuccess) return e;
   const size_t lds = m8_bytes(nw, CW, GT);
   int cus = 0;
-  e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+  e = cached_cu_count(&cus);
   if (e != hipSuccess) return e;
   const int ngroups = ((a.N + 7) / 8 + GT - 1) / GT;
   const int grid = max(1, min(ngroups, min(max(per_cu, 1), cap) * cus));
@@ -1297,7 +1298,7 @@ hipError_t launch_m8(const GemvArgs& a, int nw, int cap, hipStream_t st) {
 template <int CW>
 hipError_t launch_m8_auto(const GemvArgs& a, int nw, hipStream_t st) {
   int cus = 0;
-  hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+  hipError_t e = cached_cu_count(&cus);
   if (e != hipSuccess) return e;
   const int pc2 = m8_per_cu<CW, 2, 2>(nw, &e);
   if (e != hipSuccess) return e;
@@ -1332,7 +1333,7 @@ hipError_t launch_lds(const GemvArgs& a, hipStream_t st, int grid_cap) {
   if (attr != hipSuccess) return attr;
   const size_t lds = lds_bytes(a.K, NW, ST);
   int cus = 0;
-  hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+  hipError_t e = cached_cu_count(&cus);
   if (e != hipSuccess) return e;
   const int ngroups = (a.N + 15) / 16;
   const int grid = max(1, min(ngroups, grid_cap * cus));
@@ -1420,7 +1421,14 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
   }
   if (p.m1) {
     if (p.nw == 16 && p.rt == 2 && p.gr == 16) return launch_m1<16, 2, 16>(a, st);
-    if (p.nw == 14 && p.rt == 2 && p.gr == 16) return launch_m1<14, 2, 16>(a, st);
+    if (p.nw == 14 && p.rt == 2 && p.gr == 16) {
+      // Many 16-row groups (gate/up): when 16 x 7 is a multiple of K / 128, seven-wave
+      // workgroups, four per CU (each lane keeps its activation fragments in registers, and a
+      // group barrier waits for seven waves, not fourteen): gate/up 14.7 -> 14.2 us on MI355X
+      // against fourteen-wave workgroups, two per CU (one A/B run, same outputs).
+      if (112 % (a.K >> 7) == 0) return launch_m1<7, 2, 16>(a, st, M1Fuse{}, 4);
+      return launch_m1<14, 2, 16>(a, st);
+    }
     // Eight-wave plans run with seven waves when 16 x 7 is a multiple of K / 128 (e.g. the qkv
     // and o shapes, K / 128 = 28): each lane then meets one k-group only and keeps its
     // activation fragments in registers (qkv 5.26 -> 5.15 us, o 4.72 -> 4.55 on MI355X; same

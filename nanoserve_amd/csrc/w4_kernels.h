@@ -5,6 +5,11 @@
 
 namespace ns {
 
+// Launch-time device facts, cached per device (launch_cache.hip): the current device's CU count
+// and a kernel's occupancy (workgroups per CU) at a block size and dynamic LDS size.
+hipError_t cached_cu_count(int* cus);
+hipError_t cached_occupancy(const void* fn, int threads, size_t lds, int* per_cu);
+
 struct GemvArgs {
   const uint16_t* X;
   const uint32_t* Wq;

@@ -297,7 +297,7 @@ hipError_t launch_packed_lds(const uint16_t* X, const uint32_t* Wp, const uint16
       hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
   if (attr != hipSuccess) return attr;
   int cus = 0;
-  hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+  hipError_t e = cached_cu_count(&cus);
   if (e != hipSuccess) return e;
   const int NT = (N + 15) / 16;
   const int grid = NT < cus ? NT : cus;
@@ -310,7 +310,7 @@ template <int NW, int GW>
 hipError_t launch_packed(const uint16_t* X, const uint32_t* Wp, const uint16_t* Sp, uint16_t* Y,
                          int M, int N, int K, hipStream_t st) {
   int cus = 0;
-  hipError_t e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, 0);
+  hipError_t e = cached_cu_count(&cus);
   if (e != hipSuccess) return e;
   // measured on MI355X: two workgroups per CU with one k-group per wave, one with two
   const int NT = (N + 15) / 16;
