@@ -13,6 +13,7 @@ Tolerances, all stated against a float64 / float32 reference:
   * a replayed HIP graph equals the eager step bit for bit.
 """
 import copy
+import dataclasses
 
 import pytest
 import torch
@@ -575,3 +576,82 @@ def test_generate_graph_equals_eager(k):
     a = runner.generate(prompt, 6, use_graph=False)
     b = runner.generate(prompt, 6, use_graph=True)
     assert a == b and len(a) == 6
+
+
+def _bits16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view("uint16")
+
+
+def _oracle_layer(L, s, x0, kc, vc, pos, freq):
+    """One decoder layer of the fused decode step in float64 (oracle/decode_ref.py operators,
+    oracle.w4_oracle.linear_f64 for the W4 projections), with every intermediate rounded to bf16
+    where the kernels store it: h = bf16(x1 + d) for the layer's input row x0 [H] (bf16),
+    caches [Hk, max_len, D] (bf16, row pos overwritten with the token's k / v)."""
+    D, G = s.head_dim, s.group
+
+    def lin(a, pair):  # a: bf16-exact float64 [K] -> float64 [N]
+        Wq, S = pair
+        return torch.from_numpy(O.linear_f64(_bits16(a.reshape(1, -1).to(torch.bfloat16)),
+                                             Wq.cpu().numpy().view("uint32"), _bits16(S), G))[0]
+
+    _, a = R.rmsnorm(x0.reshape(1, -1), None, L["ln_in"], s.eps)
+    qkv = R.bf16_round(lin(R.bf16_round(a)[0], L["wqkv"]))
+    q, kk, v = R.decode_qkv(qkv.to(torch.bfloat16), L["bqkv"], s.heads, s.kv_heads, D, pos, freq)
+    kc, vc = kc.cpu().clone(), vc.cpu().clone()
+    kc[:, pos] = kk.reshape(s.kv_heads, D).to(torch.bfloat16)
+    vc[:, pos] = v.reshape(s.kv_heads, D).to(torch.bfloat16)
+    attn = R.bf16_round(R.decode_attention(q.reshape(-1).to(torch.bfloat16), kc, vc, pos + 1,
+                                           s.heads, s.kv_heads))
+    o = R.bf16_round(lin(attn, L["wo"]))
+    x1 = R.bf16_round(R._f64(x0) + o)
+    _, h2 = R.rmsnorm(x1.reshape(1, -1).to(torch.bfloat16), None, L["ln_post"], s.eps)
+    gu = R.bf16_round(lin(R.bf16_round(h2)[0], L["wgu"])).view(-1, 2, 8)  # interleaved by 8
+    act = R.bf16_round(R.swiglu(gu[:, 0].reshape(-1), gu[:, 1].reshape(-1)))
+    d = R.bf16_round(lin(act, L["wd"]))
+    return R.bf16_round(x1 + d)
+
+
+def test_runner_qwen25_7b_shape_context_1024(k):
+    """The whole 28-layer Qwen2.5-7B-shaped W4 decode step at context 1024:
+    the captured graph replays the eager step bit for bit; and the first and the last layer,
+    each run alone as a one-layer step on its own weights and cache, match the float64 oracle
+    composition of the decoder layer (residual stream after the layer; bar: the north-star
+    1e-2 * max |ref|, with bf16 activations between kernels)."""
+    s = Qwen2Shape()
+    ctx, tok, pos = 1024, 1234, 1023
+    print("runner 7B shape: building 28 layers", flush=True)
+    runner = Qwen2Runner.random(s, device=DEV, seed=7, kernels=k)
+    runner.alloc_cache(ctx)
+    g = torch.Generator(device=DEV).manual_seed(8)
+    runner.cache_k.copy_(torch.randn(runner.cache_k.shape, generator=g, device=DEV))
+    runner.cache_v.copy_(torch.randn(runner.cache_v.shape, generator=g, device=DEV))
+    eager = runner.decode(tok, pos).clone()
+    torch.cuda.synchronize()
+    assert torch.isfinite(eager.float()).all()
+    runner.capture_decode()
+    for _ in range(2):
+        replay = runner.decode(tok, pos).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(replay, eager)
+    freq = R.inv_freq(s.head_dim, s.rope_theta)
+    x0 = runner.embed[tok]
+    for li in (0, s.layers - 1):
+        print(f"runner 7B shape: layer {li} alone against the oracle", flush=True)
+        one = Qwen2Runner(dataclasses.replace(s, layers=1), runner.embed, runner.final_norm,
+                          runner.lm_head, [runner.layers[li]], k)
+        one.alloc_cache(ctx)
+        one.cache_k[0].copy_(runner.cache_k[li])
+        one.cache_v[0].copy_(runner.cache_v[li])
+        kc, vc = one.cache_k[0].clone(), one.cache_v[0].clone()
+        one.decode(tok, pos)
+        torch.cuda.synchronize()
+        # one layer: the residual stream after it is bf16(x2 + d) (x2 holds the stream after the
+        # attention block, d the down projection not yet added)
+        h = R.bf16_round(R._f64(one.x2[0]) + R._f64(one.d[0]))
+        ref = _oracle_layer(runner.layers[li], s, x0, kc, vc, pos, freq)
+        err = float((h - ref).abs().max() / ref.abs().max())
+        print(f"runner 7B shape: layer {li} max rel err {err:.2e}", flush=True)
+        assert err <= 1e-2, (li, err)
+        del one
+    del runner
+    torch.cuda.empty_cache()

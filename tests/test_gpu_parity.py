@@ -192,17 +192,28 @@ def test_gemm_small(kernels, oracle, M, N, K, G):
                          ids=["gate_up", "down"])
 @pytest.mark.parametrize("M", [512, 2048])
 def test_gemm_configs_sampled_rows(kernels, oracle, name, N, K, M):
-    """Full-size prefill GEMM on the GPU; the oracle checks 6 rows spread over M (including
-    the first and last), every column."""
+    """Full-size prefill GEMM on the GPU. The float64 oracle checks one row in every 64-row
+    band of M (the smallest M-tile of any GEMM plan, so every output tile of every plan is
+    sampled), every column; every row and column is checked against a plain torch fp32 matmul
+    on the GPU with the same bf16-staged weights, bf16_rne((q - 8) s)."""
     G = 128
+    print(f"gemm full-size {name} M={M}", flush=True)
     Wq, S = synth.weights(N, K, G, seed=N + K)
     X = synth.activations(M, K, seed=7)
     y = run_linear(kernels, X, Wq, S, G)
-    rows = np.unique(np.array([0, 1, M // 3, M // 2 + 5, M - 2, M - 1]))
+    band = 64
+    rows = np.array([b * band + (37 * b + 5) % band for b in range(M // band)])
     ref = oracle.linear_f64(X[rows], Wq, S, G)
     check_close(oracle, y[rows], ref, tight=5e-3)
     check_bf16_faithful(y[rows], oracle.linear_f64(X[rows], Wq, S, G, bf16_weights=True), 2e-5)
-    assert np.all(np.isfinite(y))
+    # all rows: torch fp32 reference on the GPU (staged weights rounded by torch's RNE cast)
+    wq, s = to_dev(Wq, torch.int32), to_dev(S, torch.bfloat16)
+    shifts = torch.arange(0, 32, 4, dtype=torch.int32, device=wq.device)
+    q = ((wq.unsqueeze(-1) >> shifts) & 0xF).reshape(N, K).float() - 8.0
+    w = (q.view(N, K // G, G) * s.float().unsqueeze(-1)).view(N, K).to(torch.bfloat16).float()
+    full = (to_dev(X, torch.bfloat16).float() @ w.t()).cpu().numpy().astype(np.float64)
+    del q, w
+    check_bf16_faithful(y, full, 3e-5)
 
 
 # ----------------------------------------------------------------- quantizer
