@@ -262,14 +262,18 @@ __device__ __forceinline__ void store_tile_lds(const f32x16_t (&acc)[MI][NJ], ui
                                                int M, int N, int m0, int n0w) {
   constexpr int WN = 32 * NJ, BMW = 32 * MI;
   const int lane = threadIdx.x & 63, ln = lane & 31, kh = lane >> 5;
+  // registers r, r + 1 (r even) are rows m, m + 1 of one column: one hardware RNE convert
+  // (v_cvt_pk_bf16_f32) rounds both
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
+      for (int r = 0; r < 16; r += 2) {
         const int row = 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
-        lds[row * LS + 32 * j + ln] = (uint16_t)f32_to_bf16_rne(acc[i][j][r]);
+        const uint32_t pk = pack_bf16x2_rne(acc[i][j][r], acc[i][j][r + 1]);
+        lds[row * LS + 32 * j + ln] = (uint16_t)pk;
+        lds[(row + 1) * LS + 32 * j + ln] = (uint16_t)(pk >> 16);
       }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's tile is in LDS
   constexpr int CPR = WN / 8;          // 16-byte chunks per row
@@ -367,8 +371,10 @@ __device__ __forceinline__ void wait_vmcnt_c() {
 // accumulators through its own part of the LDS ring (step t loads and computes block t KS + ks
 // in every group); at the end groups 1 .. KS-1 hand their accumulators to group 0 through LDS,
 // one group per round, and group 0 adds them in group order and stores the tile.
+// 256-row tiles carry 128 accumulators per lane: the launch bound asks for two workgroups per CU
+// (two waves per SIMD) so the compiler keeps them in VGPRs beside the operands.
 template <int BM, int WN, int NWN, int ST, bool SW = false, int KS = 1>
-__global__ __launch_bounds__(NWN * KS * kWave) void w4_gemm2_kernel(
+__global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 ? 2 : 1) void w4_gemm2_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ Wq,
     const uint16_t* __restrict__ S, uint16_t* __restrict__ C, int M, int N, int K, int lgG) {
   constexpr int MI = BM / 32, NJ = WN / 32, BN = WN * NWN;
@@ -571,6 +577,7 @@ constexpr TileCfg kCfgs[] = {
     {128, 128, 0.75f},  // 3: v1, BM 128, 4 waves x 32 cols
     {128, 128, 1.00f},  // 4: v2, BM 128, 4 waves x 32 cols, 3 stages
     {64, 128, 1.00f},   // 5: v2, BM 64, 4 waves x 32 cols, K split over 2 wave groups, 4 stages
+    {256, 128, 1.00f},  // 6: v2, BM 256, 4 waves x 32 cols, 2 stages, two workgroups per CU
 };
 
 }  // namespace
@@ -592,8 +599,12 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
     // 128 x 128 tiles (three workgroups per CU) unless they leave CUs idle; then 64 x 128 tiles
     // with K split over two wave groups (eight waves per workgroup; on MI355X down at M = 512:
     // 118 us against 140 for 64 x 128 without the split and 121-125 for a four-way split).
+    // 256 x 128 tiles (each wave 256 x 32: one dequantized weight word feeds eight MFMAs, not
+    // four) when there are at least four rounds of them on the chip: on MI355X gate/up at
+    // M = 2048 590 -> 555 us; with fewer tiles (gate/up M = 512, down) 128 x 128 is faster.
     const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
-    const int c = tiles < kCUs ? 5 : 4;
+    const long tiles256 = (long)((M + 255) / 256) * ((N + 127) / 128);
+    const int c = tiles < kCUs ? 5 : tiles256 >= 4 * kCUs ? 6 : 4;
     return GemmPlan{c, kCfgs[c].bm, kCfgs[c].bn};
   }
   int best = 0;
@@ -637,6 +648,10 @@ hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
       hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4, false, 2>), grid, dim3(512), 0, st, a.A, a.Wq,
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
+    case 6:
+      hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
+                         a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
     default:
       return hipErrorInvalidValue;
   }
@@ -651,6 +666,10 @@ hipError_t launch_gemm_swiglu(const GemmArgs& a, const GemmPlan& p, hipStream_t 
       return hipSuccess;
     case 5:
       hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4, true, 2>), grid, dim3(512), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 6:
+      hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2, true>), grid, dim3(256), 0, st, a.A, a.Wq,
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     default:
