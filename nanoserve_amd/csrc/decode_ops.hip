@@ -299,23 +299,15 @@ __global__ void __launch_bounds__(kAttnBlock)
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int start = split * kChunk;
 
-  // ---- issue every load first; none depends on the position, so they overlap its fetch:
-  // k (MFMA A fragments) and v (two dims per row) of the cache rows of this split, then q,
-  // bias and (fused) the token's own k / v heads
+  // ---- every load is issued first, branch-free, in the order the work needs them: the
+  // position (a scalar load), q / bias and (fused) the token's own k / v heads, then the cache
+  // rows of this split, k (MFMA A fragments) and v (two dims per row). Buffer range checks
+  // return zeros for rows past the cache and for lanes with nothing to load, so no load sits
+  // behind a branch (a branch join would make the compiler wait for every load before it).
+  constexpr uint32_t kOOB = 0x7fffffc0u;
+  const int pos = __builtin_amdgcn_readfirstlane(*pos_p);
   const int r16 = lane & 15, grp = lane >> 4;
   const int krow = 16 * w + r16;  // this lane's k row within the chunk
-  u32x4_t ka[4] = {};
-  if (start + krow < max_len) {
-    const uint16_t* src = kc + ((size_t)g * max_len + start + krow) * D + 8 * grp;
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) ka[s4] = *reinterpret_cast<const u32x4_t*>(src + 32 * s4);
-  }
-  const int in_cache = min(16, max_len - start - 16 * w);
-  const uint16_t* vbase = vc + ((size_t)g * max_len + start + 16 * w) * D + 2 * lane;
-  uint32_t vv[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    vv[i] = i < in_cache ? *reinterpret_cast<const uint32_t*>(vbase + (size_t)i * D) : 0u;
   // fused: thread t < 8R: q head t/8, rotation chunk pair t%8; then 8 threads for the k
   // head's chunk pairs and 16 for the v head's chunks
   const int nq = 8 * R;
@@ -323,39 +315,72 @@ __global__ void __launch_bounds__(kAttnBlock)
   const bool ld_k = kFused && tid >= nq && tid < nq + 8;
   const bool ld_v = kFused && tid >= nq + 8 && tid < nq + 24;
   const int c = is_q ? tid % 8 : tid - nq;
-  u32x4_t a0{}, a1{}, b0{}, b1{};
+  const int qrows = kFused ? Hq + 2 * Hk : Hq;
+  const auto qres = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(q), (short)0,
+                                                      qrows * D * 2, 0x00020000);
+  const auto bres = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(bias), (short)0,
+                                                      bias ? qrows * D * 2 : 0, 0x00020000);
+  auto ld16 = [](__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  };
+  // (fused) this thread's rotation frequency, for the angles computed once the position is
+  // known (threads 0 .. D/2 - 1)
+  float frq = 0.f;
   if constexpr (kFused) {
-    if (is_q || ld_k) {
-      const int off = (is_q ? g * R + tid / 8 : Hq + g) * D + 8 * c;
-      a0 = *reinterpret_cast<const u32x4_t*>(q + off);
-      a1 = *reinterpret_cast<const u32x4_t*>(q + off + D / 2);
-      if (bias) {
-        b0 = *reinterpret_cast<const u32x4_t*>(bias + off);
-        b1 = *reinterpret_cast<const u32x4_t*>(bias + off + D / 2);
-      }
-    } else if (ld_v) {
-      const int off = (Hq + Hk + g) * D + 8 * (tid - nq - 8);
-      a0 = *reinterpret_cast<const u32x4_t*>(q + off);
-      if (bias) b0 = *reinterpret_cast<const u32x4_t*>(bias + off);
-    }
-  } else if (tid < 8 * 16) {  // 16 dims per thread: two 16-byte loads
-    const int h = tid / 8, cc = tid % 8;
-    if (h < R) {
-      const uint16_t* src = q + (size_t)(g * R + h) * D + 16 * cc;
-      a0 = *reinterpret_cast<const u32x4_t*>(src);
-      a1 = *reinterpret_cast<const u32x4_t*>(src + 8);
-    }
+    const auto fres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(inv_freq), (short)0,
+                                                        D / 2 * 4, 0x00020000);
+    frq = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                        fres, tid < D / 2 ? 4u * tid : kOOB, 0, 0));
   }
+  u32x4_t a0, a1, b0, b1;
+  if constexpr (kFused) {
+    // element offsets of the two halves this thread rotates (q / k) or its v chunk
+    const int off = is_q ? (g * R + tid / 8) * D + 8 * c
+                  : ld_k ? (Hq + g) * D + 8 * c : (Hq + Hk + g) * D + 8 * (tid - nq - 8);
+    const bool any = is_q || ld_k || ld_v;
+    const uint32_t o0 = any ? 2u * off : kOOB, o1 = (is_q || ld_k) ? 2u * (off + D / 2) : kOOB;
+    a0 = ld16(qres, o0);
+    a1 = ld16(qres, o1);
+    b0 = ld16(bres, o0);
+    b1 = ld16(bres, o1);
+  } else {  // 16 dims per thread of head tid / 8: two 16-byte loads
+    const int h = tid / 8, cc = tid % 8;
+    const uint32_t o0 = tid < 8 * 16 && h < R ? 2u * ((g * R + h) * D + 16 * cc) : kOOB;
+    a0 = ld16(qres, o0);
+    a1 = ld16(qres, o0 == kOOB ? kOOB : o0 + 16u);
+    b0 = b1 = u32x4_t{};
+  }
+  const uint32_t head_bytes = (uint32_t)max_len * D * 2;
+  const auto kres = __builtin_amdgcn_make_buffer_rsrc(kc + (size_t)g * max_len * D, (short)0,
+                                                      (int)head_bytes, 0x00020000);
+  const auto vres = __builtin_amdgcn_make_buffer_rsrc(vc + (size_t)g * max_len * D, (short)0,
+                                                      (int)head_bytes, 0x00020000);
+  u32x4_t ka[4];
+  const uint32_t krow_off = (uint32_t)(start + krow) * D * 2 + 16u * grp;
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) ka[s4] = ld16(kres, krow_off + 64u * s4);
+  const uint32_t vrow_off = (uint32_t)(start + 16 * w) * D * 2 + 4u * lane;
+  uint32_t vv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    vv[i] = __builtin_amdgcn_raw_buffer_load_b32(vres, vrow_off + (uint32_t)i * D * 2, 0, 0);
 
   // ---- the position
-  const int pos = *pos_p;
   const int n = min(pos + 1, max_len);
-  if (n <= 0) {  // no rows: zeros (uniform over the workgroup)
-    if (split == 0)
+  if (n <= 0 || start >= n) {  // uniform over the workgroup
+    // The loaded values are inputs of this (empty) statement, so the loads are needed on this
+    // path too and stay ahead of the branch; otherwise the compiler drops them here and
+    // branches first, which puts the position's round trip in front of every load.
+    uint32_t used = a0[0] ^ a1[0] ^ b0[0] ^ b1[0] ^ __builtin_bit_cast(uint32_t, frq);
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) used ^= ka[s4][0];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) used ^= vv[i];
+    asm volatile("" ::"v"(used));
+    if (n <= 0 && split == 0)  // no rows: zeros
       for (int i = tid; i < R * D; i += kAttnBlock) out[(size_t)g * R * D + i] = 0;
     return;
   }
-  if (start >= n) return;  // uniform over the workgroup
   const int cnt = min(kChunk, n - start);
   const int nsplit = (n + kChunk - 1) / kChunk;
   // row `pos` (the token's own) is in this split when it is in the cache at all
@@ -371,7 +396,7 @@ __global__ void __launch_bounds__(kAttnBlock)
   if constexpr (kFused) {
     if (tid < D / 2) {  // the D/2 rotation angles of this position, once per workgroup
       float sn, cs;
-      sincosf(static_cast<float>(pos) * inv_freq[tid], &sn, &cs);
+      sincosf(static_cast<float>(pos) * frq, &sn, &cs);
       rot[0][tid] = cs;
       rot[1][tid] = sn;
     }

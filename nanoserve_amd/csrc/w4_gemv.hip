@@ -477,20 +477,36 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     for (int i = 0; i < XV; ++i) xa[i] = vec_load(rx, tid + i * NT);
   } else if constexpr (XM == kXAttn) {
     static_assert(XV == 1, "one activation vector per thread");
-    const int n = min(*fz.pos + 1, fz.max_len);
-    nsplit = n > 0 ? (n + kAttnDecodeChunk - 1) / kAttnDecodeChunk : 0;
+    // The position (a scalar load) and this thread's partials of the first kAttnBatch splits
+    // are all issued before any is used: the partial loads do not wait for the position (a
+    // split past it is masked after its load), so the two round trips overlap. Splits past
+    // the workspace read as zeros through the buffer range check.
+    const int posv = __builtin_amdgcn_readfirstlane(*fz.pos);
     xa[0] = vec_load(vec_rsrc(X), tid);
     const int hq = tid >> 4, d0 = 8 * (tid & 15);
+    const int smax = (fz.max_len + kAttnDecodeChunk - 1) / kAttnDecodeChunk;
+    const auto ores = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(fz.opart), (short)0,
+                                                        smax * fz.heads * 128 * 4, 0x00020000);
+    const auto mres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(fz.ml), (short)0,
+                                                        smax * fz.heads * 2 * 4, 0x00020000);
+    const bool tl = tid < KV;
 #pragma unroll
     for (int sp = 0; sp < kAttnBatch; ++sp) {
-      aml[sp] = make_float2(-INFINITY, 0.f);
-      ao[sp][0] = ao[sp][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      if (nsplit > 1 && sp < nsplit && tid < KV) {
-        aml[sp] = *reinterpret_cast<const float2*>(&fz.ml[((size_t)sp * fz.heads + hq) * 2]);
-        const f32x4_t* src = reinterpret_cast<const f32x4_t*>(
-            &fz.opart[((size_t)sp * fz.heads + hq) * 128 + d0]);
-        ao[sp][0] = src[0];
-        ao[sp][1] = src[1];
+      const uint32_t oo = tl ? 4u * (uint32_t)((sp * fz.heads + hq) * 128 + d0) : kOOB;
+      const uint32_t mo = tl ? 4u * (uint32_t)((sp * fz.heads + hq) * 2) : kOOB;
+      ao[sp][0] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ores, oo, 0, 0));
+      ao[sp][1] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ores, oo + 16u, 0, 0));
+      const auto m2 = __builtin_amdgcn_raw_buffer_load_b64(mres, mo, 0, 0);
+      aml[sp] = make_float2(__builtin_bit_cast(float, (uint32_t)m2[0]),
+                            __builtin_bit_cast(float, (uint32_t)m2[1]));
+    }
+    const int n = min(posv + 1, fz.max_len);
+    nsplit = n > 0 ? (n + kAttnDecodeChunk - 1) / kAttnDecodeChunk : 0;
+#pragma unroll
+    for (int sp = 0; sp < kAttnBatch; ++sp) {
+      if (!(nsplit > 1 && sp < nsplit && tl)) {  // masked after the load (no branch around it)
+        aml[sp] = make_float2(-INFINITY, 0.f);
+        ao[sp][0] = ao[sp][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     }
   } else {
