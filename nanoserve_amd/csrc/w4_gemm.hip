@@ -5,8 +5,8 @@
 //
 // Numerics follow the reference GEMM exactly at the point that matters: each weight is staged
 // as bf16_rne((q - 8) * s) (w4a16.cuh:190-198) before the bf16 multiply. Here that value is
-// computed as fma(q, s, -8 s) (exact, since (q - 8) s has at most 12 significant bits) and
-// rounded by the hardware RNE convert.
+// computed as fma(1024 + q, s, -1032 s) on an fp16 (1024 + q) (exact, since (q - 8) s has at
+// most 12 significant bits) and rounded by the hardware RNE convert.
 //
 // Design:
 //  * v_mfma_f32_32x32x16_bf16 with A = activations (row i = m), B = weights (column j = n).
@@ -35,27 +35,33 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) {
 }
 
 // One packed word -> 8 staged weights bf16_rne((q - 8) * s), natural k order, as 4 bf16x2.
-// The nibbles are isolated into bytes with one mask each (lo: even nibbles, hi: odd nibbles;
-// vmask = 0x0F0F0F0F in a VGPR) and converted by v_cvt_f32_ubyte0..3, which read a byte
-// directly; fma(q, s, -8 s) is (q - 8) s exactly; v_cvt_pk_bf16_f32 rounds to nearest even.
-template <int B>
-__device__ __forceinline__ float cvt_ubyte(uint32_t v) {
-  float f;
-  if (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(v));
-  if (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(v));
-  if (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(v));
-  if (B == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(v));
-  return f;
+// One v_and_or_b32 per two nibbles builds an fp16 pair (1024 + q_a, 1024 + q_b): the nibbles
+// land in the low mantissa bits of two halves whose exponent field (0x6400) means 1024
+// (vmask = 0x000F000F in a VGPR, w shifted by 0/4/8/12 bits). The fp32 fma takes the fp16
+// operand widened in the instruction itself (v_fma_mix_f32), so a weight costs half a logic op
+// and one fma: fma(1024 + q, s, -1032 s) = (q - 8) s, exact because s is a bf16 (1032 s and
+// (1024 + q) s fit fp32's 24-bit significand) for |s| < 2^118; v_cvt_pk_bf16_f32 then rounds
+// to nearest even. The quantizer's scales (absmax / 7 of bf16 weights) are far below that
+// bound.
+__device__ __forceinline__ uint32_t and_or_s(uint32_t a, uint32_t vmask, uint32_t sbits) {
+  uint32_t d;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(vmask), "s"(sbits));
+  return d;
 }
 
-__device__ __forceinline__ u32x4_t dequant_word_bf16(uint32_t w, uint32_t vmask, float s, float ns8) {
-  const uint32_t t0 = w & vmask;         // nibbles 0, 2, 4, 6 in bytes 0..3
-  const uint32_t t1 = (w >> 4) & vmask;  // nibbles 1, 3, 5, 7
+__device__ __forceinline__ u32x4_t dequant_word_bf16(uint32_t w, uint32_t vmask, float s,
+                                                     float ns1032) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  constexpr uint32_t kE1024 = 0x64006400u;  // fp16 1024.0 in both halves
+  const h2_t h0 = __builtin_bit_cast(h2_t, and_or_s(w, vmask, kE1024));        // q0, q4
+  const h2_t h1 = __builtin_bit_cast(h2_t, and_or_s(w >> 4, vmask, kE1024));   // q1, q5
+  const h2_t h2 = __builtin_bit_cast(h2_t, and_or_s(w >> 8, vmask, kE1024));   // q2, q6
+  const h2_t h3 = __builtin_bit_cast(h2_t, and_or_s(w >> 12, vmask, kE1024));  // q3, q7
   u32x4_t d;
-  d[0] = pack_bf16x2_rne(__builtin_fmaf(cvt_ubyte<0>(t0), s, ns8), __builtin_fmaf(cvt_ubyte<0>(t1), s, ns8));
-  d[1] = pack_bf16x2_rne(__builtin_fmaf(cvt_ubyte<1>(t0), s, ns8), __builtin_fmaf(cvt_ubyte<1>(t1), s, ns8));
-  d[2] = pack_bf16x2_rne(__builtin_fmaf(cvt_ubyte<2>(t0), s, ns8), __builtin_fmaf(cvt_ubyte<2>(t1), s, ns8));
-  d[3] = pack_bf16x2_rne(__builtin_fmaf(cvt_ubyte<3>(t0), s, ns8), __builtin_fmaf(cvt_ubyte<3>(t1), s, ns8));
+  d[0] = pack_bf16x2_rne(__builtin_fmaf((float)h0[0], s, ns1032), __builtin_fmaf((float)h1[0], s, ns1032));
+  d[1] = pack_bf16x2_rne(__builtin_fmaf((float)h2[0], s, ns1032), __builtin_fmaf((float)h3[0], s, ns1032));
+  d[2] = pack_bf16x2_rne(__builtin_fmaf((float)h0[1], s, ns1032), __builtin_fmaf((float)h1[1], s, ns1032));
+  d[3] = pack_bf16x2_rne(__builtin_fmaf((float)h2[1], s, ns1032), __builtin_fmaf((float)h3[1], s, ns1032));
   return d;
 }
 
@@ -145,25 +151,25 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm_kernel(
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   uint32_t vmask;
-  asm volatile("v_mov_b32 %0, 0x0F0F0F0F" : "=v"(vmask));
+  asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(vmask));
 
   // One 64-k block: four k16 steps, software-pipelined: while the 16 MFMAs of step s run, the
   // A fragments of step s + 1 are read from LDS and its B fragments dequantized; the group
   // barriers interleave them (1 MFMA, a few VALU ops, an LDS read, ...).
   auto compute = [&](int stage, const WRegs& r) {
     const uint16_t* as = As[stage];
-    float sc[NJ], ns8[NJ];
+    float sc[NJ], nb[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       sc[j] = bf16_bits_to_f32(r.s[j]);
-      ns8[j] = -8.f * sc[j];
+      nb[j] = -1032.f * sc[j];
     }
     u32x4_t af[2][MI], bf[2][NJ];
 #pragma unroll
     for (int i = 0; i < MI; ++i)
       af[0][i] = *reinterpret_cast<const u32x4_t*>(&as[(32 * i + ln) * LDA + 32 * kh]);
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) bf[0][j] = dequant_word_bf16(r.w[j][0], vmask, sc[j], ns8[j]);
+    for (int j = 0; j < NJ; ++j) bf[0][j] = dequant_word_bf16(r.w[j][0], vmask, sc[j], nb[j]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int cur = s & 1, nxt = cur ^ 1;
@@ -172,7 +178,7 @@ __global__ __launch_bounds__(NWN * kWave) void w4_gemm_kernel(
         for (int i = 0; i < MI; ++i)
           af[nxt][i] = *reinterpret_cast<const u32x4_t*>(&as[(32 * i + ln) * LDA + 32 * kh + 8 * (s + 1)]);
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) bf[nxt][j] = dequant_word_bf16(r.w[j][s + 1], vmask, sc[j], ns8[j]);
+        for (int j = 0; j < NJ; ++j) bf[nxt][j] = dequant_word_bf16(r.w[j][s + 1], vmask, sc[j], nb[j]);
       }
 #pragma unroll
       for (int i = 0; i < MI; ++i)
@@ -452,7 +458,7 @@ __global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 ? 2 : 1) void w4_gemm2_
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   uint32_t vmask;
-  asm volatile("v_mov_b32 %0, 0x0F0F0F0F" : "=v"(vmask));
+  asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(vmask));
   // LDS offset (elements) of this lane's A fragment: row 32 i + ln, chunk 4 kh + s (swizzled)
   auto a_frag = [&](const uint16_t* as, int i, int s) {
     const int row = 32 * i + ln;
@@ -462,17 +468,17 @@ __global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 ? 2 : 1) void w4_gemm2_
 
   auto compute = [&](int stage, const WRegs& r) {
     const uint16_t* as = &As[(stage * KS + ks) * STAGE];
-    float sc[NJ], ns8[NJ];
+    float sc[NJ], nb[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       sc[j] = bf16_bits_to_f32(r.s[j]);
-      ns8[j] = -8.f * sc[j];
+      nb[j] = -1032.f * sc[j];
     }
     u32x4_t af[2][MI], bf[2][NJ];
 #pragma unroll
     for (int i = 0; i < MI; ++i) af[0][i] = a_frag(as, i, 0);
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) bf[0][j] = dequant_word_bf16(r.w[j][0], vmask, sc[j], ns8[j]);
+    for (int j = 0; j < NJ; ++j) bf[0][j] = dequant_word_bf16(r.w[j][0], vmask, sc[j], nb[j]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int cur = s & 1, nxt = cur ^ 1;
@@ -480,7 +486,7 @@ __global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 ? 2 : 1) void w4_gemm2_
 #pragma unroll
         for (int i = 0; i < MI; ++i) af[nxt][i] = a_frag(as, i, s + 1);
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) bf[nxt][j] = dequant_word_bf16(r.w[j][s + 1], vmask, sc[j], ns8[j]);
+        for (int j = 0; j < NJ; ++j) bf[nxt][j] = dequant_word_bf16(r.w[j][s + 1], vmask, sc[j], nb[j]);
       }
 #pragma unroll
       for (int i = 0; i < MI; ++i)
