@@ -66,6 +66,8 @@ def parse():
                    help="only the dominant-kernel launches (gate_up, M=1), e.g. under a profiler")
     p.add_argument("--gemm-only", action="store_true",
                    help="only the prefill GEMM launches (config 4), e.g. under a profiler")
+    p.add_argument("--m1-only", action="store_true",
+                   help="only the config-2 set (the four layers at M=1), e.g. under a profiler")
     p.add_argument("--m8-only", action="store_true",
                    help="only the config-3 set (the four layers at M=8), e.g. under a profiler")
     p.add_argument("--decode-only", action="store_true",
@@ -440,6 +442,16 @@ def main():
         print(json.dumps({"config3_m8_set": m8_set(), "launches": 4 * (4 * copies) * 4 + 4}), flush=True)
         return
 
+    if args.m1_only:
+        g1 = graph_of(lambda i: step(x1, i), 4 * copies)
+        time_graph(g1)
+        ms1 = statistics.median(time_graph(g1) for _ in range(3)) / (4 * copies)
+        bytes_set = sum(synth.gemv_bytes(1, N, K, G) for _, N, K in layers)
+        print(json.dumps({"config2_m1_set": {
+            "gbs": round(bytes_set / (ms1 * 1e-3) / 1e9, 1), "us_per_step": round(ms1 * 1e3, 3)},
+            "launches": 4 * (4 * copies) * 4 + 4}), flush=True)
+        return
+
     bytes_m1 = sum(synth.gemv_bytes(1, N, K, G) for _, N, K in layers)
     gate = None if args.dominant_only else correctness_gate()
     if gate is not None and not gate["pass"]:
@@ -469,7 +481,7 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": profiled_traffic(TRAFFIC_PROFILE),
-                "kernel": "w4_gemv_m1_kernel<14, 2, 16, 0, 0, 4, true> (gate_up 37888x3584, M=1)",
+                "kernel": "w4_gemv_m1_kernel<7, 2, 16, 0, 0, 4, true> (gate_up 37888x3584, M=1)",
                 "bytes_per_launch": bytes_gu, "avg_launch_us": round(ms_gu * 1e3, 3)}
 
     if args.dominant_only:

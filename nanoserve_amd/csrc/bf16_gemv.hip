@@ -25,7 +25,11 @@ namespace {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kLmWaves = 8;  // waves per workgroup
+// Waves per workgroup. At the largest K (MAXKB 16) a wave holds three 64-register row buffers
+// (current row, next row, activation); four-wave workgroups let it use the accumulation
+// registers as well, so nothing spills to memory.
+template <int MAXKB>
+constexpr int lm_waves() { return MAXKB > 8 ? 4 : 8; }
 
 // The vector elements are copied to scalars before the bit casts: this compiler, given
 // __builtin_bit_cast of a vector element directly, emits the first element's register for all
@@ -42,13 +46,14 @@ __device__ __forceinline__ float dot8(const u32x4_t& a, const u32x4_t& b, float 
 
 // MAXKB: 512-element blocks per row the registers are sized for; KB = ceil(K / 512) <= MAXKB.
 template <int MAXKB, bool kNorm>
-__global__ void __launch_bounds__(kLmWaves * kWave)
+__global__ void __launch_bounds__(lm_waves<MAXKB>() * kWave)
     bf16_gemv_kernel(const uint16_t* __restrict__ X, const uint16_t* __restrict__ res,
                      const uint16_t* __restrict__ radd, const uint16_t* __restrict__ nw,
                      float eps, const uint16_t* __restrict__ W, uint16_t* __restrict__ Y, int N,
                      int K) {
   const int lane = threadIdx.x & (kWave - 1);
   const int KB = (K + 511) >> 9;
+  constexpr int kLmWaves = lm_waves<MAXKB>();
   const long long wave0 = (long long)blockIdx.x * kLmWaves + (threadIdx.x >> 6);
   const long long nwaves = (long long)gridDim.x * kLmWaves;
 
@@ -123,10 +128,12 @@ template <int MAXKB>
 void launch_bf16(const uint16_t* X, const uint16_t* res, const uint16_t* radd,
                  const uint16_t* nw, float eps, const uint16_t* W, uint16_t* Y, int N, int K,
                  hipStream_t st) {
+  constexpr int kLmWaves = lm_waves<MAXKB>();
   int cus = 0;
   if (cached_cu_count(&cus) != hipSuccess) cus = 256;  // the launch's own error is reported
   const long long blocks = (static_cast<long long>(N) + kLmWaves - 1) / kLmWaves;
-  const int grid = static_cast<int>(blocks < 2LL * cus ? blocks : 2LL * cus);
+  const long long cap = (MAXKB > 8 ? 1LL : 2LL) * cus;  // workgroups resident at once
+  const int grid = static_cast<int>(blocks < cap ? blocks : cap);
   if (res)
     hipLaunchKernelGGL((bf16_gemv_kernel<MAXKB, true>), dim3(grid), dim3(kLmWaves * kWave), 0, st,
                        X, res, radd, nw, eps, W, Y, N, K);
