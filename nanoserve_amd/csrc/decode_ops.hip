@@ -386,10 +386,10 @@ __global__ void __launch_bounds__(kAttnBlock)
   // row `pos` (the token's own) is in this split when it is in the cache at all
   const bool has_new = kFused && pos < max_len && pos - start < kChunk;
   const bool k_is_new = has_new && start + krow == pos;
+  // rows of this wave inside the position; the value loop skips the others (their loads read
+  // whatever the cache holds), and does not touch vv before then, so the value rows are not
+  // waited for until they are used
   const int rows = min(16, cnt - 16 * w);
-#pragma unroll
-  for (int i = 0; i < 16; ++i)
-    if (i >= rows) vv[i] = 0u;  // rows past the position: no stale values in the sums
   const bool is_k = has_new && ld_k;
   const bool is_v = has_new && ld_v;
 
@@ -461,16 +461,18 @@ __global__ void __launch_bounds__(kAttnBlock)
     }
   }
   __syncthreads();
-  if (has_new) {  // the token's own row comes from LDS
+  // the token's own row comes from LDS; its value row is swapped in where the value loop
+  // reads vv (a substitution here would make every value load complete first)
+  int inew = -1;
+  uint32_t vnw = 0u;
+  if (has_new) {
     if (k_is_new) {
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4)
         ka[s4] = *reinterpret_cast<const u32x4_t*>(&knew[32 * s4 + 8 * grp]);
     }
-    const int inew = pos - start - 16 * w;
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      if (i == inew) vv[i] = *reinterpret_cast<const uint32_t*>(&vnew[2 * lane]);
+    inew = pos - start - 16 * w;
+    vnw = *reinterpret_cast<const uint32_t*>(&vnew[2 * lane]);
   }
 
   // ---- scores: S[row][head] for the wave's 16 rows and 16 head slots
@@ -517,7 +519,8 @@ __global__ void __launch_bounds__(kAttnBlock)
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     if (i < rows) {
-      const float v0 = __uint_as_float(vv[i] << 16), v1 = __uint_as_float(vv[i] & 0xffff0000u);
+      const uint32_t vi = i == inew ? vnw : vv[i];
+      const float v0 = __uint_as_float(vi << 16), v1 = __uint_as_float(vi & 0xffff0000u);
       const f32x4_t p0 = *reinterpret_cast<const f32x4_t*>(&ps[16 * w + i][0]);
       const f32x4_t p1 = *reinterpret_cast<const f32x4_t*>(&ps[16 * w + i][4]);
 #pragma unroll
