@@ -364,6 +364,8 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt_c() {
   // s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0], expcnt, lgkmcnt, vmcnt[5:4])
@@ -379,7 +381,7 @@ __device__ __forceinline__ void wait_vmcnt_c() {
 // one group per round, and group 0 adds them in group order and stores the tile.
 // 256-row tiles carry 128 accumulators per lane: the launch bound asks for two workgroups per CU
 // (two waves per SIMD) so the compiler keeps them in VGPRs beside the operands.
-template <int BM, int WN, int NWN, int ST, bool SW = false, int KS = 1>
+template <int BM, int WN, int NWN, int ST, bool SW = false, int KS = 1, int WD = 1>
 __global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 ? 2 : 1) void w4_gemm2_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ Wq,
     const uint16_t* __restrict__ S, uint16_t* __restrict__ C, int M, int N, int K, int lgG) {
@@ -507,6 +509,40 @@ __global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 ? 2 : 1) void w4_gemm2_
     }
   };
 
+  if constexpr (WD > 1) {
+    // Weights and scales WD - 1 blocks further ahead than the activation tiles: a ring of
+    // WR = ST + WD - 1 register slots. Per block the activation tile is issued first, then the
+    // weights (scheduling barriers keep that order), so when block kb starts only the weight
+    // loads of the block after the tile of kb, and the (ST - 2) blocks' loads between, may still
+    // be in flight: the explicit wait counts exactly those, and the weights of block kb were
+    // issued before its tile.
+    constexpr int WR = ST + WD - 1;
+    constexpr int UNR = ST * WR / gcd_c(ST, WR);  // the loop body sees every (stage, slot) pair
+    WRegs wr[WR];
+#pragma unroll
+    for (int p = 0; p < WR - 1; ++p) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (p < ST - 1) issue_a(p, p * KS + ks);
+      __builtin_amdgcn_sched_barrier(0);
+      issue_w(wr[p], p * KS + ks);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int t0 = 0; t0 < T; t0 += UNR) {
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) {
+        const int kb = (t0 + u) * KS + ks;
+        wait_vmcnt_c<2 * NJ + (ST - 2) * (IPW + 2 * NJ)>();  // block kb's tile has landed
+        lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        issue_a((u + ST - 1) % ST, kb + (ST - 1) * KS);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_w(wr[(u + WR - 1) % WR], kb + (WR - 1) * KS);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kb < KB) compute(u % ST, wr[u % WR]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else {
   // Explicit waits count only the LDS-DMA activation loads (IPW per wave per block): those stay
   // in program order, while the compiler may move the weight and scale loads (whose register
   // uses it guards itself). Counting only later DMA loads can over-wait, never under-wait.
@@ -531,6 +567,7 @@ __global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 ? 2 : 1) void w4_gemm2_
       if (kb < KB) compute(u, wr[u]);
       __builtin_amdgcn_sched_barrier(0);
     }
+  }
   }
 
   wait_vmcnt_c<0>();  // the trailing out-of-range loads have landed before the LDS is reused
@@ -627,6 +664,11 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
   return GemmPlan{best, kCfgs[best].bm, kCfgs[best].bn};
 }
 
+// Weight prefetch distance of the 128- and 256-row plans, in blocks beyond the activation tiles
+// (WD): 3 measured best on MI355X (gate/up M = 2048 537-541 -> 520-523 us, M = 512 159-161 ->
+// 153-157, down M = 2048 313 -> 308, against 1; 4 and 5 no better; same outputs bit for bit).
+constexpr int kWeightAhead = 3;
+
 hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
   const dim3 grid((a.N + p.bn - 1) / p.bn, (a.M + p.bm - 1) / p.bm);
   switch (p.cfg) {
@@ -647,7 +689,7 @@ hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
                          a.C, a.M, a.N, a.K, a.G);
       return hipSuccess;
     case 4:
-      hipLaunchKernelGGL((w4_gemm2_kernel<128, 32, 4, 3>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
+      hipLaunchKernelGGL((w4_gemm2_kernel<128, 32, 4, 3, false, 1, kWeightAhead>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
                          a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     case 5:
@@ -655,7 +697,7 @@ hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     case 6:
-      hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
+      hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2, false, 1, kWeightAhead>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
                          a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     default:
@@ -667,7 +709,7 @@ hipError_t launch_gemm_swiglu(const GemmArgs& a, const GemmPlan& p, hipStream_t 
   const dim3 grid((a.N + p.bn - 1) / p.bn, (a.M + p.bm - 1) / p.bm);
   switch (p.cfg) {
     case 4:
-      hipLaunchKernelGGL((w4_gemm2_kernel<128, 32, 4, 3, true>), grid, dim3(256), 0, st, a.A, a.Wq,
+      hipLaunchKernelGGL((w4_gemm2_kernel<128, 32, 4, 3, true, 1, kWeightAhead>), grid, dim3(256), 0, st, a.A, a.Wq,
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     case 5:
@@ -675,7 +717,7 @@ hipError_t launch_gemm_swiglu(const GemmArgs& a, const GemmPlan& p, hipStream_t 
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     case 6:
-      hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2, true>), grid, dim3(256), 0, st, a.A, a.Wq,
+      hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2, true, 1, kWeightAhead>), grid, dim3(256), 0, st, a.A, a.Wq,
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     default:
