@@ -249,10 +249,11 @@ def main():
     def decode_step(reps=40, ctx=1024):
         """config 5: one decode step of a random-init W4A16 Qwen2.5-7B (28 layers, fused QKV and
         gate+up, bf16 lm_head) at context 1024 with a bf16 KV cache filled with N(0,1); the step
-        is one HIP graph replay: per layer ns_w4_gemv_decode (q/k/v, add + RMSNorm in),
+        is one HIP graph replay: ns_decode_embed (embedding row + the position's rotation
+        table), then per layer ns_w4_gemv_decode (q/k/v, add + RMSNorm in),
         ns_decode_qkv_attention, ns_w4_gemv_decode_attn (o), ns_w4_gemv_decode (gate/up, add +
         RMSNorm in, SwiGLU out), ns_w4_gemv_decode (down); then ns_bf16_gemv (final add + RMSNorm
-        + lm_head) and torch's embedding gather."""
+        + lm_head)."""
         from nanoserve_amd.qwen import Qwen2Runner, Qwen2Shape
 
         shape = Qwen2Shape()

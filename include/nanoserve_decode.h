@@ -110,12 +110,27 @@ int ns_decode_attention_noalloc(const void* q, const void* k_cache, const void* 
  * attention of the rotated q over rows 0 .. min(*pos + 1, max_len) - 1. Same arguments,
  * workspace and return codes as those two. merge == 0 leaves the per-split partial results in
  * the workspace instead of merging them (out is then written only when the rows fit one
- * split): ns_w4_gemv_decode_attn merges them while it loads its activation.
+ * split): ns_w4_gemv_decode_attn merges them while it loads its activation. rot: NULL, or the
+ * rotation table [2][D/2] fp32 (cos, then sin) of this position written by ns_decode_embed on
+ * the same stream: the angles are then read from it instead of being computed in every
+ * workgroup (same values, same outputs). 16-byte aligned.
  */
 int ns_decode_qkv_attention(const void* qkv, const void* bias, const void* inv_freq,
                             const int* pos, void* k_cache, void* v_cache, void* out, void* work,
                             size_t work_bytes, int Hq, int Hk, int D, int max_len, int merge,
-                            void* stream);
+                            const float* rot, void* stream);
+
+/*
+ * No counterpart in the reference's C ABI (its runner gathers the embedding row with PyTorch,
+ * python/nanoserve/qwen.py:141, and computes the rotation angles inside its RoPE): the start
+ * of a decode step. x [H] bf16 = embed [vocab][H] row *tok (a token id outside [0, vocab) gives
+ * a zero row), and rot [2][D/2] fp32 = cos, sin of fp32(*pos) * inv_freq[i] for i < D/2, the
+ * table ns_decode_qkv_attention takes for every layer of the step. tok and pos are device int32
+ * so a captured graph replays at any token and position. Returns -2 for vocab <= 0, H <= 0,
+ * H % 8 != 0, D % 16 != 0, D > 512, NULL or misaligned pointers (embed, x, rot 16-byte aligned).
+ */
+int ns_decode_embed(const int* tok, const int* pos, const void* embed, int vocab, int H,
+                    const void* inv_freq, int D, void* x, float* rot, void* stream);
 
 /*
  * No counterpart in the reference's C ABI: the decode-step GEMV (M = 1) with its neighbouring

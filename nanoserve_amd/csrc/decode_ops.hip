@@ -277,7 +277,8 @@ constexpr int kMaxGroup = 8;  // query heads per kv head (score columns 0..7 of 
 template <bool kFused>
 __global__ void __launch_bounds__(kAttnBlock)
     decode_attn_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ bias,
-                       const float* __restrict__ inv_freq, uint16_t* __restrict__ kc,
+                       const float* __restrict__ inv_freq, const float* __restrict__ rot_tab,
+                       uint16_t* __restrict__ kc,
                        uint16_t* __restrict__ vc, const int* __restrict__ pos_p,
                        uint16_t* __restrict__ out, float* __restrict__ opart,
                        float* __restrict__ ml, int Hq, int Hk, int max_len, float qscale) {
@@ -323,14 +324,26 @@ __global__ void __launch_bounds__(kAttnBlock)
   auto ld16 = [](__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
   };
-  // (fused) this thread's rotation frequency, for the angles computed once the position is
-  // known (threads 0 .. D/2 - 1)
+  // (fused) the rotation angles: with a table (rot_tab [2][D/2] = cos, sin of this position,
+  // written once per decode step by ns_decode_embed), the cosines and sines of the 8 pairs a
+  // q / k thread rotates are loaded with everything else; without one, threads 0 .. D/2 - 1
+  // load their frequency and compute the angles once the position is known.
+  const bool tab = kFused && rot_tab != nullptr;  // uniform
   float frq = 0.f;
+  u32x4_t tc0{}, tc1{}, ts0{}, ts1{};
   if constexpr (kFused) {
     const auto fres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(inv_freq), (short)0,
-                                                        D / 2 * 4, 0x00020000);
+                                                        tab ? 0 : D / 2 * 4, 0x00020000);
     frq = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                         fres, tid < D / 2 ? 4u * tid : kOOB, 0, 0));
+    const auto tres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(rot_tab), (short)0,
+                                                        tab ? D * 4 : 0, 0x00020000);
+    const int tci = tid < nq ? tid % 8 : tid - nq;  // pair chunk of a q or k thread
+    const uint32_t to = tid < nq + 8 ? 32u * (uint32_t)tci : kOOB;
+    tc0 = ld16(tres, to);
+    tc1 = ld16(tres, to == kOOB ? kOOB : to + 16u);
+    ts0 = ld16(tres, to == kOOB ? kOOB : to + 4u * (D / 2));
+    ts1 = ld16(tres, to == kOOB ? kOOB : to + 4u * (D / 2) + 16u);
   }
   u32x4_t a0, a1, b0, b1;
   if constexpr (kFused) {
@@ -371,7 +384,8 @@ __global__ void __launch_bounds__(kAttnBlock)
     // The loaded values are inputs of this (empty) statement, so the loads are needed on this
     // path too and stay ahead of the branch; otherwise the compiler drops them here and
     // branches first, which puts the position's round trip in front of every load.
-    uint32_t used = a0[0] ^ a1[0] ^ b0[0] ^ b1[0] ^ __builtin_bit_cast(uint32_t, frq);
+    uint32_t used = a0[0] ^ a1[0] ^ b0[0] ^ b1[0] ^ __builtin_bit_cast(uint32_t, frq) ^ tc0[0] ^
+                    tc1[0] ^ ts0[0] ^ ts1[0];
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) used ^= ka[s4][0];
 #pragma unroll
@@ -394,7 +408,7 @@ __global__ void __launch_bounds__(kAttnBlock)
   const bool is_v = has_new && ld_v;
 
   if constexpr (kFused) {
-    if (tid < D / 2) {  // the D/2 rotation angles of this position, once per workgroup
+    if (!tab && tid < D / 2) {  // the D/2 rotation angles of this position, once per workgroup
       float sn, cs;
       sincosf(static_cast<float>(pos) * frq, &sn, &cs);
       rot[0][tid] = cs;
@@ -405,7 +419,8 @@ __global__ void __launch_bounds__(kAttnBlock)
       *reinterpret_cast<u32x4_t*>(&qb[h][16 * cc]) = u32x4_t{};
       *reinterpret_cast<u32x4_t*>(&qb[h][16 * cc + 8]) = u32x4_t{};
     }
-    __syncthreads();
+    if (!tab) __syncthreads();  // the angles in LDS (uniform branch; the q slots are read after
+                                // the next barrier)
     if (is_q || is_k) {
       float lo[8], hi[8];
       unpack8(a0, lo);
@@ -422,7 +437,9 @@ __global__ void __launch_bounds__(kAttnBlock)
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float cs = rot[0][8 * c + e], sn = rot[1][8 * c + e];
+        const uint32_t tcs = e < 4 ? tc0[e & 3] : tc1[e & 3], tsn = e < 4 ? ts0[e & 3] : ts1[e & 3];
+        const float cs = tab ? __builtin_bit_cast(float, tcs) : rot[0][8 * c + e];
+        const float sn = tab ? __builtin_bit_cast(float, tsn) : rot[1][8 * c + e];
         const float x1 = lo[e], x2 = hi[e];
         lo[e] = x1 * cs - x2 * sn;
         hi[e] = x2 * cs + x1 * sn;
@@ -651,6 +668,33 @@ __global__ void __launch_bounds__(kBlock)
   }
 }
 
+// ------------------------------------------------------------------ decode-step start
+// The token's embedding row is copied to x, 16 bytes per thread through buffers whose range
+// checks turn a token id outside [0, vocab) into a zero row and drop stores past the row; and
+// workgroup 0 computes the step's rotation table rot [2][D/2] = cos, sin of fp32(pos) *
+// inv_freq[i], the values the attention kernel would otherwise compute in every workgroup of
+// every layer (same expression, same compiler, so the same bits).
+__global__ void __launch_bounds__(kBlock)
+    decode_embed_kernel(const int* __restrict__ tok_p, const int* __restrict__ pos_p,
+                        const uint16_t* __restrict__ embed, int vocab, int H,
+                        const float* __restrict__ inv_freq, int half, uint16_t* __restrict__ x,
+                        float* __restrict__ rot) {
+  const int tok = __builtin_amdgcn_readfirstlane(*tok_p);
+  const bool ok = tok >= 0 && tok < vocab;
+  const uint32_t rb = 2u * (uint32_t)H;
+  const auto er = bytes_rsrc(embed + (ok ? (size_t)tok * H : 0), ok ? rb : 0u);
+  const auto xr = bytes_rsrc(x, rb);
+  const uint32_t off = 16u * (blockIdx.x * kBlock + threadIdx.x);
+  st16(xr, off, ld16(er, off));
+  if (blockIdx.x == 0 && static_cast<int>(threadIdx.x) < half) {
+    const int pos = __builtin_amdgcn_readfirstlane(*pos_p);
+    float sn, cs;
+    sincosf(static_cast<float>(pos) * inv_freq[threadIdx.x], &sn, &cs);
+    rot[threadIdx.x] = cs;
+    rot[half + threadIdx.x] = sn;
+  }
+}
+
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 int last_status() { return static_cast<int>(hipGetLastError()); }
@@ -683,7 +727,7 @@ int attn_check(int Hq, int Hk, int D, int max_len, size_t work_bytes, const void
 template <bool kFused>
 int launch_attn(const void* q, const void* bias, const void* inv_freq, void* kc, void* vc,
                 const int* pos, void* out, void* work, int Hq, int Hk, int max_len,
-                hipStream_t st, bool merge = true) {
+                hipStream_t st, bool merge = true, const float* rot = nullptr) {
   const size_t splits = attn_splits(max_len);
   float* opart = static_cast<float*>(work);
   float* ml = opart + splits * Hq * kHeadDim;
@@ -691,7 +735,7 @@ int launch_attn(const void* q, const void* bias, const void* inv_freq, void* kc,
   const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(Hk));
   hipLaunchKernelGGL(decode_attn_kernel<kFused>, grid, dim3(kAttnBlock), 0, st,
                      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(bias),
-                     static_cast<const float*>(inv_freq), static_cast<uint16_t*>(kc),
+                     static_cast<const float*>(inv_freq), rot, static_cast<uint16_t*>(kc),
                      static_cast<uint16_t*>(vc), pos, static_cast<uint16_t*>(out), opart, ml, Hq,
                      Hk, max_len, qscale);
   if (merge && splits > 1) {
@@ -878,16 +922,31 @@ int ns_decode_attention_noalloc(const void* q, const void* k_cache, const void* 
 int ns_decode_qkv_attention(const void* qkv, const void* bias, const void* inv_freq,
                             const int* pos, void* k_cache, void* v_cache, void* out, void* work,
                             size_t work_bytes, int Hq, int Hk, int D, int max_len, int merge,
-                            void* stream) {
+                            const float* rot, void* stream) {
   const int rc = ns::attn_check(Hq, Hk, D, max_len, work_bytes, work);
   if (rc) return rc;
   if (!qkv || !inv_freq || !pos || !k_cache || !v_cache || !out) return -2;
   if (!ns::aligned(qkv, 16) || !ns::aligned(bias, 16) || !ns::aligned(inv_freq, 4) ||
       !ns::aligned(pos, 4) || !ns::aligned(k_cache, 16) || !ns::aligned(v_cache, 16) ||
-      !ns::aligned(out, 2))
+      !ns::aligned(out, 2) || !ns::aligned(rot, 16))
     return -2;
   return ns::launch_attn<true>(qkv, bias, inv_freq, k_cache, v_cache, pos, out, work, Hq, Hk,
-                               max_len, static_cast<hipStream_t>(stream), merge != 0);
+                               max_len, static_cast<hipStream_t>(stream), merge != 0, rot);
+}
+
+int ns_decode_embed(const int* tok, const int* pos, const void* embed, int vocab, int H,
+                    const void* inv_freq, int D, void* x, float* rot, void* stream) {
+  if (vocab <= 0 || H <= 0 || H % 8 || D <= 0 || D % 16 || D > 512) return -2;
+  if (!tok || !pos || !embed || !inv_freq || !x || !rot) return -2;
+  if (!ns::aligned(tok, 4) || !ns::aligned(pos, 4) || !ns::aligned(embed, 16) ||
+      !ns::aligned(inv_freq, 4) || !ns::aligned(x, 16) || !ns::aligned(rot, 16))
+    return -2;
+  const unsigned grid = static_cast<unsigned>((H / 8 + ns::kBlock - 1) / ns::kBlock);
+  hipLaunchKernelGGL(ns::decode_embed_kernel, dim3(grid), dim3(ns::kBlock), 0,
+                     static_cast<hipStream_t>(stream), tok, pos,
+                     static_cast<const uint16_t*>(embed), vocab, H,
+                     static_cast<const float*>(inv_freq), D / 2, static_cast<uint16_t*>(x), rot);
+  return ns::last_status();
 }
 
 }  // extern "C"

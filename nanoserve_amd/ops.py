@@ -30,7 +30,8 @@ SIGNATURES = {
     "ns_decode_attention_workspace": [_I32, _I32, _I32, _I32],
     "ns_decode_attention": [_VP, _VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32, _I32, _VP],
     "ns_decode_qkv_attention": [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32,
-                                _I32, _I32, _VP],
+                                _I32, _I32, _VP, _VP],
+    "ns_decode_embed": [_VP, _VP, _VP, _I32, _I32, _VP, _I32, _VP, _VP, _VP],
     "ns_w4_gemv_decode_attn": [_VP, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _I32, _I32, _I32, _VP],
 }
 SIGNATURES["ns_w4_gemv_decode"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _I32, _I32, _I32,
@@ -54,6 +55,13 @@ def _require_gpu_tensor(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
         raise ValueError(f"{name} must be a GPU tensor (got device {t.device})")
     if t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+
+
+def _rot_ptr(rot, head_dim):
+    _require_gpu_tensor(rot, "rot", torch.float32)
+    if not rot.is_contiguous() or rot.numel() != head_dim:
+        raise ValueError("rot must be a contiguous [2, head_dim / 2] float32 tensor")
+    return rot.data_ptr()
 
 
 def _check_out(out: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
@@ -309,11 +317,13 @@ class Kernels:
         return out
 
     def decode_qkv_attention(self, qkv, bias, inv_freq, pos, k_cache, v_cache, n_heads,
-                             n_kv_heads, head_dim, work, out=None, merge=True):
+                             n_kv_heads, head_dim, work, out=None, merge=True, rot=None):
         """decode_qkv followed by decode_attention in one launch, qkv left unchanged: bias +
         RoPE of the q heads, the token's k / v row appended to the cache at pos[0], attention
         over rows 0 .. pos[0]. Returns out [1, Hq * D] bf16. With ``merge=False`` the split
-        partials stay in ``work`` for gemv_decode_attn (out is written only for one split)."""
+        partials stay in ``work`` for gemv_decode_attn (out is written only for one split).
+        ``rot``: the step's rotation table from ``decode_embed`` (same outputs, fewer
+        instructions per workgroup)."""
         _require_gpu_tensor(qkv, "qkv", torch.bfloat16)
         _require_gpu_tensor(inv_freq, "inv_freq", torch.float32)
         _require_gpu_tensor(pos, "pos", torch.int32)
@@ -332,9 +342,32 @@ class Kernels:
             qkv.data_ptr(), None if bias is None else bias.data_ptr(), inv_freq.data_ptr(),
             pos.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
             work.data_ptr(), work.numel(), n_heads, n_kv_heads, head_dim, k_cache.shape[-2],
-            1 if merge else 0, self._stream())
+            1 if merge else 0, None if rot is None else _rot_ptr(rot, head_dim), self._stream())
         self._check(rc, "ns_decode_qkv_attention")
         return out
+
+    def decode_embed(self, tok, pos, embed, inv_freq, x=None, rot=None):
+        """Start of a decode step (no counterpart in the reference, whose runner gathers the
+        row with F.embedding, qwen.py:141): x [1, H] = embed[tok[0]] (zeros for an id outside
+        the table) and rot [2, D/2] fp32 = cos, sin of pos[0] * inv_freq, the table
+        decode_qkv_attention takes. Returns (x, rot)."""
+        _require_gpu_tensor(tok, "tok", torch.int32)
+        _require_gpu_tensor(pos, "pos", torch.int32)
+        _require_gpu_tensor(embed, "embed", torch.bfloat16)
+        _require_gpu_tensor(inv_freq, "inv_freq", torch.float32)
+        if not embed.is_contiguous() or embed.dim() != 2:
+            raise ValueError("embed must be a contiguous [vocab, H] tensor")
+        vocab, H = embed.shape
+        D = 2 * inv_freq.numel()
+        if x is None:
+            x = torch.empty((1, H), dtype=torch.bfloat16, device=embed.device)
+        if rot is None:
+            rot = torch.empty((2, D // 2), dtype=torch.float32, device=embed.device)
+        rc = self.lib.ns_decode_embed(tok.data_ptr(), pos.data_ptr(), embed.data_ptr(), vocab, H,
+                                      inv_freq.data_ptr(), D, x.data_ptr(), _rot_ptr(rot, D),
+                                      self._stream())
+        self._check(rc, "ns_decode_embed")
+        return x, rot
 
     def gemv_decode_attn(self, attn_out, work, pos, max_len, n_heads, Wq, S, group=128,
                          out=None):

@@ -141,8 +141,10 @@ class Qwen2Runner:
         # one-token decode state: device-resident token id and position, static activations
         H, I = shape.hidden, shape.intermediate
         bf = dict(dtype=torch.bfloat16, device=self.dev)
-        self.tok = torch.zeros(1, dtype=torch.int64, device=self.dev)
+        self.tok = torch.zeros(1, dtype=torch.int32, device=self.dev)
         self.pos = torch.zeros(1, dtype=torch.int32, device=self.dev)
+        # the step's rotation table (cos, sin of pos * inv_freq), written by decode_embed
+        self.rot = torch.empty(2, D // 2, dtype=torch.float32, device=self.dev)
         self.x = torch.empty(1, H, **bf)
         self.x2 = torch.empty(1, H, **bf)
         self.h = torch.empty(1, H, **bf)
@@ -274,6 +276,8 @@ class Qwen2Runner:
         """One decode step on self.tok / self.pos (device tensors) into self.logits. Launches
         only; no allocation, no host synchronisation, so it can be captured.
 
+        First ns_decode_embed: the token's embedding row, and the position's rotation table,
+        which every layer's attention then reads instead of computing the angles itself.
         Per layer five kernels: the q/k/v GEMV with the residual add + input RMSNorm fused
         into its activation load, the attention (bias + RoPE + KV append + attention over
         128-row splits of the cache), the o GEMV, which merges the attention's splits as it
@@ -282,7 +286,7 @@ class Qwen2Runner:
         buffers (a fused GEMV reads one and one of its workgroups writes the other)."""
         s, k = self.shape, self.k
         D, G, eps = s.head_dim, s.group, s.eps
-        torch.index_select(self.embed, 0, self.tok, out=self.x)
+        k.decode_embed(self.tok, self.pos, self.embed, self.inv_freq, x=self.x, rot=self.rot)
         resid, spare = self.x, self.x2
         pending = None  # the addend not yet in the residual stream (the last down output)
         for li, L in enumerate(self.layers):
@@ -294,7 +298,7 @@ class Qwen2Runner:
                 resid, spare = spare, resid
             k.decode_qkv_attention(self.qkv[0], L["bqkv"], self.inv_freq, self.pos,
                                    self.cache_k[li], self.cache_v[li], s.heads, s.kv_heads, D,
-                                   self.work, out=self.attn, merge=False)
+                                   self.work, out=self.attn, merge=False, rot=self.rot)
             k.gemv_decode_attn(self.attn, self.work, self.pos, self.max_len, s.heads, *L["wo"],
                                G, out=self.o)
             k.gemv_decode(*L["wgu"], G, res=resid, r=self.o, norm_w=L["ln_post"], eps=eps,

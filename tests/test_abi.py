@@ -37,7 +37,7 @@ def test_header_declares_the_reference_entry_points():
         "ns_w4_linear", "ns_w4_quantize", "ns_w4_repack", "ns_w4_linear_packed",
         "ns_rmsnorm", "ns_rope", "ns_swiglu",
         "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention",
-        "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn",
+        "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn", "ns_decode_embed",
         "ns_bf16_gemv", "ns_w4_gptq_workspace", "ns_w4_gptq", "ns_w4_linear_swiglu",
         "ns_probe_read", "ns_probe_empty", "ns_decode_attention_noalloc"])
 
@@ -167,9 +167,9 @@ def test_decode_attention_workspace_and_rejects(k):
     assert call(q=None) == -2
     assert call(work=P + 4) == -2
 
-    def fused(work_bytes=ws, Hq=28, Hk=4, D=128, L=1024, qkv=P, work=P):
+    def fused(work_bytes=ws, Hq=28, Hk=4, D=128, L=1024, qkv=P, work=P, rot=None):
         return k.lib.ns_decode_qkv_attention(qkv, None, P, P, P, P, P, work, work_bytes, Hq, Hk,
-                                             D, L, 1, None)
+                                             D, L, 1, rot, None)
 
     assert fused(work_bytes=ws - 1) == -2
     assert fused(D=64) == -2
@@ -177,6 +177,25 @@ def test_decode_attention_workspace_and_rejects(k):
     assert fused(qkv=None) == -2
     assert fused(qkv=P + 8) == -2
     assert fused(work=None) == -2
+    assert fused(rot=P + 4) == -2               # the rotation table is read 16 bytes at a time
+
+
+def test_decode_embed_rejects(k):
+    """ns_decode_embed checks its sizes and pointers before any HIP call."""
+    def call(vocab=1000, H=3584, D=128, tok=P, pos=P, embed=P, x=P, rot=P):
+        return k.lib.ns_decode_embed(tok, pos, embed, vocab, H, P, D, x, rot, None)
+
+    assert call(vocab=0) == -2
+    assert call(H=0) == -2
+    assert call(H=3583) == -2
+    assert call(D=120) == -2
+    assert call(D=1024) == -2
+    for name in ("tok", "pos", "embed", "x", "rot"):
+        assert call(**{name: None}) == -2, name
+    assert call(embed=P + 8) == -2
+    assert call(x=P + 8) == -2
+    assert call(rot=P + 4) == -2
+    assert call(tok=P + 2) == -2
 
 
 def test_decode_attention_noalloc_rejects(k):

@@ -197,6 +197,56 @@ def test_decode_qkv_attention(k, Hq, Hk, with_bias):
               atol=2e-3)
 
 
+@pytest.mark.parametrize("H,vocab,D", [(3584, 152064, 128), (896, 1000, 64), (8, 3, 16)])
+def test_decode_embed(k, H, vocab, D):
+    """ns_decode_embed: x is the token's embedding row bit for bit (a zero row for ids outside
+    the table) and rot holds cos, sin of fp32(pos) * inv_freq within 2 fp32 ulp of float64
+    cos / sin of that same fp32 angle (the oracle's angle), at positions 0 .. 131071."""
+    embed = rnd(vocab, H, seed=90)
+    freq = R.inv_freq(D, 1000000.0)
+    for tok, pos in [(0, 0), (vocab - 1, 1), (vocab // 2, 1023), (vocab // 3, 131071), (-1, 5),
+                     (vocab, 7)]:
+        print(f"decode_embed H={H} vocab={vocab} D={D} tok={tok} pos={pos}", flush=True)
+        t = torch.tensor([tok], dtype=torch.int32, device=DEV)
+        p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+        x, rot = k.decode_embed(t, p, embed, freq.to(DEV))
+        torch.cuda.synchronize()
+        want = embed[tok] if 0 <= tok < vocab else torch.zeros_like(embed[0])
+        assert torch.equal(x.reshape(-1), want)
+        ang = (torch.tensor(float(pos), dtype=torch.float32) * freq.float()).double()
+        got = rot.double().cpu()
+        ulp = 2.0 ** -23
+        assert ((got[0] - torch.cos(ang)).abs() <= 2 * ulp).all()
+        assert ((got[1] - torch.sin(ang)).abs() <= 2 * ulp).all()
+
+
+@pytest.mark.parametrize("Hq,Hk", [(28, 4), (7, 1)])
+def test_decode_qkv_attention_rotation_table(k, Hq, Hk):
+    """With the step's rotation table from ns_decode_embed, the fused attention gives the same
+    output bits and the same appended cache rows as computing the angles itself, at positions
+    in the first split, across splits and past the cache."""
+    D, max_len = 128, 600
+    qn, kn = Hq * D, Hk * D
+    freq = R.inv_freq(D, 1000000.0).to(DEV)
+    embed = rnd(16, 64, seed=91)
+    for i, pos in enumerate([0, 127, 128, 513, 599, 700]):
+        print(f"decode_qkv_attention rotation table Hq={Hq} Hk={Hk} pos={pos}", flush=True)
+        qkv = rnd(qn + 2 * kn, seed=92 + i, scale=0.5)
+        bias = rnd(qn + 2 * kn, seed=99 + i, scale=0.25)
+        kc, vc = rnd(Hk, max_len, D, seed=93), rnd(Hk, max_len, D, seed=94)
+        kc2, vc2 = kc.clone(), vc.clone()
+        p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+        t = torch.tensor([3], dtype=torch.int32, device=DEV)
+        _, rot = k.decode_embed(t, p, embed, freq)
+        wa = k.decode_attention_workspace(Hq, Hk, D, max_len)
+        wb = k.decode_attention_workspace(Hq, Hk, D, max_len)
+        a = k.decode_qkv_attention(qkv, bias, freq, p, kc, vc, Hq, Hk, D, wa)
+        b = k.decode_qkv_attention(qkv, bias, freq, p, kc2, vc2, Hq, Hk, D, wb, rot=rot)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b)
+        assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+
+
 def _attn_chunk(k):
     """Cache rows per attention split: the first length at which one more row adds a split
     to the workspace."""
