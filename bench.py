@@ -190,9 +190,31 @@ def main():
             del w
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
+        q = quantization_case()
+        ok = (all(v <= 1e-2 for v in errs.values()) and q["codes_bit_exact"] and
+              abs(q["quant_error_pct"] - q["oracle_pct"]) <= 0.05)
         return {"max_rel_err": {k: float(f"{v:.3e}") for k, v in errs.items()},
-                "tolerance": 1e-2, "pass": all(v <= 1e-2 for v in errs.values()),
-                "reference": "torch fp32 dequant + fp32 matmul on the GPU"}
+                "tolerance": 1e-2, "pass": ok,
+                "reference": "torch fp32 dequant + fp32 matmul on the GPU", "quantization": q}
+
+    def quantization_case():
+        """The reference's correctness case (bench_w4a16.cu:143-196: N = 256, K = 512, G = 128,
+        128 hash-filled activation rows, its inputs frozen in tests/golden/quant_case.npz): the
+        GPU quantizer's codes and scales against the fixture's, and the 4-bit quantization error
+        ||Y_w4 - Y_bf16|| / ||Y_bf16|| of the GPU GEMM's output against the bf16 weights' fp32
+        product -- the figure the reference prints per run (7.05 %)."""
+        z = np.load(os.path.join(ROOT, "tests", "golden", "quant_case.npz"))
+        W = dev_bits(z["W"], torch.bfloat16)
+        X = dev_bits(z["X"], torch.bfloat16)
+        wq, s = kern.w4_quantize(W, int(z["G"]))
+        torch.cuda.synchronize()
+        same = (np.array_equal(wq.cpu().view(torch.int32).numpy().view(np.uint32), z["Wq"]) and
+                np.array_equal(s.cpu().view(torch.int16).numpy().view(np.uint16), z["S"]))
+        y_w4 = kern.w4_linear(X, wq, s, int(z["G"])).float()
+        y_bf16 = X.float() @ W.float().t()
+        err = float(((y_w4 - y_bf16).norm() / y_bf16.norm()).item()) * 100
+        return {"codes_bit_exact": bool(same), "quant_error_pct": round(err, 2),
+                "oracle_pct": round(float(z["quant_error_pct"]), 2), "reference_pct": 7.05}
 
     def ceiling():
         """The launch floor (an empty kernel in a graph, per launch) and the read-only stream

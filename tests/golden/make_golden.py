@@ -12,6 +12,10 @@ Files:
                 activations X (rows 0..7), y_exact = fp32-dequant double-accumulated outputs,
                 y_staged = the same with bf16-staged weights (the reference GEMM's semantics)
   edge_case.npz a small non-default format: G=32, K=96, N=48, M=3 (bf16 bits throughout)
+  quant_case.npz the same correctness case's bf16 inputs, W [256, 512] and all 128 rows of X,
+                with its 4-bit quantization error ||Y_w4 - Y_bf16|| / ||Y_bf16|| in percent
+                (the reference prints it per run, bench/bench_w4a16.cu:192-196: 7.05 %); read by
+                bench.py, which measures the same figure with the GPU quantizer and GEMM
 """
 import os
 import sys
@@ -44,7 +48,18 @@ def edge_case():
                 y_exact=orc.linear_f64(X, Wq, S, G).astype(np.float32))
 
 
-CASES = {"ref_case": ref_case, "edge_case": edge_case}
+def quant_case():
+    N, K, G, Mmax = 256, 512, 128, 128
+    W = orc.hash_fill(N * K, 11, 0.05).reshape(N, K)
+    X = orc.hash_fill(Mmax * K, 12, 1.0).reshape(Mmax, K)
+    Wq, S = orc.quantize(W, G)
+    y_w4 = orc.linear_f64(X, Wq, S, G).astype(np.float32)
+    y_bf16 = orc.linear_dense_f64(X, orc.bf16_to_f32(W))
+    return dict(N=N, K=K, G=G, W=W, X=X, Wq=Wq, S=S,
+                quant_error_pct=np.float64(100 * orc.rel_fro(y_w4, y_bf16)))
+
+
+CASES = {"ref_case": ref_case, "edge_case": edge_case, "quant_case": quant_case}
 
 
 def main():
