@@ -246,7 +246,7 @@ __global__ void __launch_bounds__(kBlock)
 }
 
 // ------------------------------------------------------------------ decode attention
-// Workgroup (s, g) covers cache rows [s*kChunk, (s+1)*kChunk) of kv head g for all R = Hq/Hk
+// Workgroup (s, g, z) covers cache rows [s*kChunk, (s+1)*kChunk) of kv head g for all R = Hq/Hk
 // query heads of the group. It computes the split's max m (base-2 logits), sum l of
 // 2^(logit - m) and unnormalised output sum_p 2^(logit_p - m) v_p in fp32. A single split
 // normalises and writes the output itself; otherwise the splits' partials go to the workspace
@@ -265,8 +265,12 @@ __global__ void __launch_bounds__(kBlock)
 // (A = k rows, lane l: row l%16, dims 32s + 8(l/16)..+7; B = q heads, lane l: head l%16, same
 // dims; D: lane l holds rows 4(l/16)+r of head l%16), so each lane owns one head and the
 // per-head max and sum need two lane swaps instead of a 64-lane reduction per head; the values
-// are a VALU loop, each lane two dims of each of the wave's rows (one 4-byte load per row: the
-// wave reads each 256-byte row whole), probabilities broadcast from LDS.
+// are a VALU loop, probabilities broadcast from LDS. Each split is served by two workgroups
+// (blockIdx.z), each producing half of the value dimensions: both compute the same scores and
+// softmax (the k rows are read twice, a small cost next to the value loop), lane l of a wave
+// owns dimension 64 z + l of each of the wave's rows (a 2-byte load per row), so each
+// workgroup's value loop and output reduction are half as long; workgroup z = 0 alone appends
+// the token's row to the cache and writes the split's (max, sum).
 constexpr int kAttnWaves = kAttnDecodeChunk / 16;  // waves per attention workgroup, 16 rows each
 constexpr int kAttnBlock = kAttnWaves * kWave;
 constexpr int kChunk = kAttnDecodeChunk;   // cache rows per split
@@ -290,12 +294,13 @@ __global__ void __launch_bounds__(kAttnBlock)
   __shared__ __attribute__((aligned(16))) float ps[kChunk][RP];
   __shared__ float red_m[NWV][16];
   __shared__ float red_l[NWV][16];
-  __shared__ float ored[NWV][RP][D];
+  __shared__ float ored[NWV][RP][D / 2];
   __shared__ float rot[2][D / 2];
   __shared__ __attribute__((aligned(16))) uint16_t knew[D];
   __shared__ __attribute__((aligned(16))) uint16_t vnew[D];
 
   const int split = blockIdx.x, g = blockIdx.y;
+  const int dh = blockIdx.z;  // which half of the value dimensions this workgroup produces
   const int R = Hq / Hk;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int start = split * kChunk;
@@ -372,11 +377,11 @@ __global__ void __launch_bounds__(kAttnBlock)
   const uint32_t krow_off = (uint32_t)(start + krow) * D * 2 + 16u * grp;
 #pragma unroll
   for (int s4 = 0; s4 < 4; ++s4) ka[s4] = ld16(kres, krow_off + 64u * s4);
-  const uint32_t vrow_off = (uint32_t)(start + 16 * w) * D * 2 + 4u * lane;
+  const uint32_t vrow_off = (uint32_t)(start + 16 * w) * D * 2 + 2u * (D / 2 * dh + lane);
   uint32_t vv[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i)
-    vv[i] = __builtin_amdgcn_raw_buffer_load_b32(vres, vrow_off + (uint32_t)i * D * 2, 0, 0);
+    vv[i] = __builtin_amdgcn_raw_buffer_load_b16(vres, vrow_off + (uint32_t)i * D * 2, 0, 0);
 
   // ---- the position
   const int n = min(pos + 1, max_len);
@@ -391,7 +396,7 @@ __global__ void __launch_bounds__(kAttnBlock)
 #pragma unroll
     for (int i = 0; i < 16; ++i) used ^= vv[i];
     asm volatile("" ::"v"(used));
-    if (n <= 0 && split == 0)  // no rows: zeros
+    if (n <= 0 && split == 0 && dh == 0)  // no rows: zeros
       for (int i = tid; i < R * D; i += kAttnBlock) out[(size_t)g * R * D + i] = 0;
     return;
   }
@@ -452,9 +457,11 @@ __global__ void __launch_bounds__(kAttnBlock)
       } else {
         *reinterpret_cast<u32x4_t*>(&knew[8 * c]) = plo;
         *reinterpret_cast<u32x4_t*>(&knew[D / 2 + 8 * c]) = phi;
-        uint16_t* row = kc + ((size_t)g * max_len + pos) * D;
-        *reinterpret_cast<u32x4_t*>(row + 8 * c) = plo;
-        *reinterpret_cast<u32x4_t*>(row + D / 2 + 8 * c) = phi;
+        if (dh == 0) {  // one of the two workgroups of the split appends the row
+          uint16_t* row = kc + ((size_t)g * max_len + pos) * D;
+          *reinterpret_cast<u32x4_t*>(row + 8 * c) = plo;
+          *reinterpret_cast<u32x4_t*>(row + D / 2 + 8 * c) = phi;
+        }
       }
     } else if (is_v) {
       u32x4_t v = a0;
@@ -468,7 +475,7 @@ __global__ void __launch_bounds__(kAttnBlock)
       }
       const int cv = tid - nq - 8;
       *reinterpret_cast<u32x4_t*>(&vnew[8 * cv]) = v;
-      *reinterpret_cast<u32x4_t*>(vc + ((size_t)g * max_len + pos) * D + 8 * cv) = v;
+      if (dh == 0) *reinterpret_cast<u32x4_t*>(vc + ((size_t)g * max_len + pos) * D + 8 * cv) = v;
     }
   } else {
     if (tid < 8 * 16) {
@@ -489,7 +496,7 @@ __global__ void __launch_bounds__(kAttnBlock)
         ka[s4] = *reinterpret_cast<const u32x4_t*>(&knew[32 * s4 + 8 * grp]);
     }
     inew = pos - start - 16 * w;
-    vnw = *reinterpret_cast<const uint32_t*>(&vnew[2 * lane]);
+    vnw = vnew[D / 2 * dh + lane];
   }
 
   // ---- scores: S[row][head] for the wave's 16 rows and 16 head slots
@@ -529,37 +536,34 @@ __global__ void __launch_bounds__(kAttnBlock)
   if (grp == 0) red_l[w][h] = l;
   __syncthreads();
 
-  // ---- values: lane owns dims 2 lane, 2 lane + 1
-  float acc[RP][2];
+  // ---- values: lane owns dim D/2 dh + lane
+  float acc[RP];
 #pragma unroll
-  for (int hh = 0; hh < RP; ++hh) acc[hh][0] = acc[hh][1] = 0.f;
+  for (int hh = 0; hh < RP; ++hh) acc[hh] = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     if (i < rows) {
       const uint32_t vi = i == inew ? vnw : vv[i];
-      const float v0 = __uint_as_float(vi << 16), v1 = __uint_as_float(vi & 0xffff0000u);
+      const float v0 = __uint_as_float(vi << 16);
       const f32x4_t p0 = *reinterpret_cast<const f32x4_t*>(&ps[16 * w + i][0]);
       const f32x4_t p1 = *reinterpret_cast<const f32x4_t*>(&ps[16 * w + i][4]);
 #pragma unroll
       for (int hh = 0; hh < 4; ++hh) {
-        acc[hh][0] = fmaf(p0[hh], v0, acc[hh][0]);
-        acc[hh][1] = fmaf(p0[hh], v1, acc[hh][1]);
-        acc[hh + 4][0] = fmaf(p1[hh], v0, acc[hh + 4][0]);
-        acc[hh + 4][1] = fmaf(p1[hh], v1, acc[hh + 4][1]);
+        acc[hh] = fmaf(p0[hh], v0, acc[hh]);
+        acc[hh + 4] = fmaf(p1[hh], v0, acc[hh + 4]);
       }
     }
   }
 #pragma unroll
-  for (int hh = 0; hh < RP; ++hh)
-    *reinterpret_cast<float2*>(&ored[w][hh][2 * lane]) = make_float2(acc[hh][0], acc[hh][1]);
+  for (int hh = 0; hh < RP; ++hh) ored[w][hh][lane] = acc[hh];
   __syncthreads();
 
   const bool single = nsplit == 1;
-  for (int i = tid; i < R * D; i += kAttnBlock) {
-    const int hh = i / D, d = i % D;
+  for (int i = tid; i < R * D / 2; i += kAttnBlock) {
+    const int hh = i / (D / 2), d = D / 2 * dh + i % (D / 2);
     float o = 0.f;
 #pragma unroll
-    for (int k = 0; k < NWV; ++k) o += ored[k][hh][d];
+    for (int k = 0; k < NWV; ++k) o += ored[k][hh][d - D / 2 * dh];
     if (single) {
       float lt = 0.f;
 #pragma unroll
@@ -569,7 +573,7 @@ __global__ void __launch_bounds__(kAttnBlock)
       opart[((size_t)split * Hq + g * R + hh) * D + d] = o;
     }
   }
-  if (!single && tid < R) {
+  if (!single && dh == 0 && tid < R) {
     float mt = red_m[0][tid], lt = 0.f;
 #pragma unroll
     for (int k = 0; k < NWV; ++k) {
@@ -732,7 +736,7 @@ int launch_attn(const void* q, const void* bias, const void* inv_freq, void* kc,
   float* opart = static_cast<float*>(work);
   float* ml = opart + splits * Hq * kHeadDim;
   const float qscale = 1.4426950408889634f / sqrtf(static_cast<float>(kHeadDim));  // log2(e)/sqrt(D)
-  const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(Hk));
+  const dim3 grid(static_cast<unsigned>(splits), static_cast<unsigned>(Hk), 2u);
   hipLaunchKernelGGL(decode_attn_kernel<kFused>, grid, dim3(kAttnBlock), 0, st,
                      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(bias),
                      static_cast<const float*>(inv_freq), rot, static_cast<uint16_t*>(kc),
