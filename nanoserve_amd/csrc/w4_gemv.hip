@@ -401,9 +401,11 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
 //    so D[j][j] = sum x * (q - 8) as in the reference dequant.
 //  * The piece's scale is S[flat piece index] (S is [N][K / 128], i.e. one bf16 per piece in
 //    the same order): 16 consecutive bf16 per block, one 2-byte buffer load per lane.
-//  * Workgroups are persistent over GR-row groups (GR = 16, or 8: GR C pieces must fill whole
-//    blocks); the GR C / 16 blocks of a group are dealt
-//    to the NW waves round-robin. Each diagonal lane writes scale * D[j][j] to an LDS partial
+//  * Workgroups are persistent over GR-row groups; the ceil(GR C / 16) blocks of a group are
+//    dealt to the NW waves round-robin. A group's pieces are contiguous in Wq, so its blocks
+//    start at any 64-byte piece boundary, and when GR C is not a multiple of 16 the lanes of
+//    the last block past the group's end write to the dummy slot (their loads read the next
+//    group's pieces, or zeros past the buffer). Each diagonal lane writes scale * D[j][j] to an LDS partial
 //    table (double-buffered by group parity); after the group's barrier, 16 lanes per row sum
 //    the row's C partials and wave (i % NW) writes Y.
 //  * Blocks stream through a ring of R register slots (R - 1 blocks in flight per wave),
@@ -428,9 +430,11 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15, kg = lane >> 4;
-  const int ngroups = (N + GR - 1) / GR;
+  const int GRr = GR > 0 ? GR : fz.rows;  // rows per group (GR == 0: chosen at launch)
+  const int ngroups = (N + GRr - 1) / GRr;
   const int gstep = gridDim.x;
-  const int NBG = GR * C / 16;  // 1 KiB blocks per group
+  const int NP = GRr * C;          // pieces per group
+  const int NBG = (NP + 15) >> 4;  // 1 KiB blocks per group (the last one may be partial)
   const int nbp = R * ((NBG + NW * R - 1) / (NW * R));
 
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
@@ -445,10 +449,10 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   auto issue = [&](u32x4_t& w, uint32_t& sc) {
     const int b = wv + NW * ir;
     const bool live = gr < ngroups && b < NBG;
-    const uint32_t blk = (uint32_t)(gr * NBG + b);
+    const uint32_t p0 = (uint32_t)(gr * NP + 16 * b);  // first piece of the block
     w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                        wres, vw, live ? 1024u * blk : kOOB, kStreamAux));
-    sc = __builtin_amdgcn_raw_buffer_load_b16(sres, vs, live ? 32u * blk : kOOB, kStreamAux);
+                                        wres, vw, live ? 64u * p0 : kOOB, kStreamAux));
+    sc = __builtin_amdgcn_raw_buffer_load_b16(sres, vs, live ? 2u * p0 : kOOB, kStreamAux);
     if (++ir == nbp) {
       ir = 0;
       gr += gstep;
@@ -525,6 +529,9 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
 
   u32x4_t ring[R];
   uint32_t rsc[R];
+  // (one workgroup per CU) the vector memory pipeline returns loads in issue order, so the
+  // activation, issued by every wave before this barrier, does not wait for weight blocks
+  if (fz.xfirst) __builtin_amdgcn_s_barrier();
 #pragma unroll
   for (int u = 0; u < R; ++u) issue(ring[u], rsc[u]);
   __builtin_amdgcn_sched_barrier(0);
@@ -648,7 +655,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   const bool diag = kg == (j >> 2);
   const int dr = j & 3;
   const bool s1 = dr == 1, s2 = dr == 2, s3 = dr == 3;
-  float* dummy = part + 2 * GR * C + lane;
+  float* dummy = part + 2 * NP + lane;
   const int c_first = (16 * wv + j) % C;
   const int c_step = (16 * NW) % C;
   // FC (the launcher checks that 16 NW is a multiple of C, e.g. gate/up: C = 28, NW = 14):
@@ -664,7 +671,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   }
   int g = blockIdx.x;
   for (int it = 0; g < ngroups; ++it, g += gstep) {
-    float* pt = part + (it & 1) * GR * C + j;
+    float* pt = part + (it & 1) * NP + j;
     int c = c_first;
     auto block = [&](auto fixed, int u, int b) {
       f32x4_t t;
@@ -686,8 +693,8 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
       float v = s1 ? t[1] : t[0];
       v = s2 ? t[2] : v;
       v = s3 ? t[3] : v;
-      float* dst = diag && b < NBG ? pt + 16 * b : dummy;
-      *dst = bf16_bits_to_f32(rsc[u] & 0xffffu) * v;
+      float* dst = diag && 16 * b + j < NP ? pt + 16 * b : dummy;
+      *dst = __uint_as_float(rsc[u] << 16) * v;  // the 16-bit load zero-extends
       if constexpr (!decltype(fixed)::value) {
         c += c_step;
         c = c >= C ? c - C : c;
@@ -710,18 +717,18 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     // C = 148): a wave per row, its lanes taking the row's partials c = lane, lane + 64, ...
     // (one lane-wise pass, then a wave sum) instead of one wave walking C / 4 partials per lane
     // for all the rows
-    constexpr bool kWideReduce = NW == 16 && YM != kYSwiglu;
+    constexpr bool kWideReduce = (NW == 16 || GR > 16 || GR == 0) && YM != kYSwiglu;
     if constexpr (kWideReduce) {
-      for (int rw = wv; rw < GR; rw += NW) {
-        const float* pr = part + (it & 1) * GR * C + rw * C;
+      for (int rw = wv; rw < GRr; rw += NW) {
+        const float* pr = part + (it & 1) * NP + rw * C;
         float v = 0.f;
         for (int cc = lane; cc < C; cc += kWave) v += pr[cc];
         v = wave_sum(v);
-        const int n = GR * g + rw;
+        const int n = GRr * g + rw;
         if (lane == 0 && n < N) Y[n] = (uint16_t)f32_to_bf16_rne(v);
       }
     } else if (wv == it % NW) {
-      const float* pr = part + (it & 1) * GR * C;
+      const float* pr = part + (it & 1) * NP;
       float v = 0.f;
       if (j < GR)
         for (int cc = kg; cc < C; cc += 4) v += pr[j * C + cc];
@@ -1249,7 +1256,9 @@ hipError_t launch_m1_fc(const GemvArgs& a, hipStream_t st, const M1Fuse& fz, int
   static const hipError_t attr =
       hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
   if (attr != hipSuccess) return attr;
-  const size_t lds = m1_bytes(a.K, GR);
+  const int rows = GR > 0 ? GR : fz.rows;
+  if (rows <= 0) return hipErrorInvalidValue;
+  const size_t lds = m1_bytes(a.K, rows);
   int per_cu = 0;
   hipError_t e = cached_occupancy(fn, NW * kWave, lds, &per_cu);
   if (e != hipSuccess) return e;
@@ -1258,7 +1267,7 @@ hipError_t launch_m1_fc(const GemvArgs& a, hipStream_t st, const M1Fuse& fz, int
   if (e != hipSuccess) return e;
   // wpc workgroups per CU (two unless the plan says otherwise): more resident waves only
   // lengthen the memory queues.
-  const int ngroups = (a.N + GR - 1) / GR;
+  const int ngroups = (a.N + rows - 1) / rows;
   const int grid = max(1, min(ngroups, min(max(per_cu, 1), wpc) * cus));
   hipLaunchKernelGGL((w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV, FC>), dim3(grid), dim3(NW * kWave), lds,
                      st, a.X, a.Wq, a.S, a.Y, a.N, a.K, fz);
@@ -1372,6 +1381,53 @@ void m1_choose(int N, int K, int& nw, int& r) {
     nw = 8;
 }
 
+// Launch layout of the M = 1 kernel. The plain and the fused entry points take the same layout
+// for a shape, so they sum its partials in the same order and give the same bits.
+struct M1Layout {
+  int nw = 8;           // waves per workgroup
+  int gr = 16;          // rows per group as a template argument (0: `rows`, chosen here)
+  int rows = 0;
+  int wpc = 2;          // workgroups per CU
+  bool xfirst = false;  // activation loads ahead of the workgroup's weight loads
+};
+
+// * Long rows (K / 128 >= 64, e.g. down): 16 waves per 16-row group; when the groups fit one
+//   per CU, each CU holds one workgroup and its activation goes first.
+// * Many groups (gate/up): the streaming plans, four seven-wave workgroups per CU when
+//   16 x 7 is a multiple of K / 128.
+// * Layers whose weights give every CU at most 32 blocks of 1 KiB (qkv, o): one workgroup per
+//   CU with ceil(N / CUs) rows, all of its blocks in flight at once (two per wave), activation
+//   first. On MI355X: qkv 5.40 -> 4.96 us, o 5.19 -> 4.59 us against the 8-row / 16-row
+//   groups at two workgroups per CU; down 10.73 -> 10.07 us with its activation first (one
+//   interleaved run, same outputs).
+// * Otherwise eight waves per 16-row group (8-row groups when 16-row ones would give each CU
+//   only one or two), two workgroups per CU.
+hipError_t m1_layout(int N, int K, M1Layout* L) {
+  int cus = 0;
+  const hipError_t e = cached_cu_count(&cus);
+  if (e != hipSuccess) return e;
+  const int C = K >> 7, groups16 = (N + 15) / 16;
+  M1Layout l;
+  if (C >= 64) {
+    l.nw = 16;
+    l.xfirst = groups16 <= cus;
+  } else if (groups16 >= 1024 && C >= 14) {
+    l.nw = 112 % C == 0 ? 7 : 14;
+    l.wpc = l.nw == 7 ? 4 : 2;
+  } else if (const int rows = (N + cus - 1) / cus; (rows * C + 15) / 16 <= 32) {
+    const int blocks = (rows * C + 15) / 16;
+    l.nw = 224 % C == 0 && blocks <= 28 ? 14 : 16;
+    l.gr = 0;
+    l.rows = rows;
+    l.wpc = 1;
+    l.xfirst = true;
+  } else {
+    l.gr = groups16 > 256 && groups16 < 512 && C % 2 == 0 ? 8 : 16;
+  }
+  *L = l;
+  return hipSuccess;
+}
+
 }  // namespace
 
 // Register-X kernel limits: scale staging must fit comfortably in LDS next to the reduction.
@@ -1436,24 +1492,29 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
     return hipSuccess;
   }
   if (p.m1) {
-    if (p.nw == 16 && p.rt == 2 && p.gr == 16) return launch_m1<16, 2, 16>(a, st);
-    if (p.nw == 14 && p.rt == 2 && p.gr == 16) {
-      // Many 16-row groups (gate/up): when 16 x 7 is a multiple of K / 128, seven-wave
-      // workgroups, four per CU (each lane keeps its activation fragments in registers, and a
-      // group barrier waits for seven waves, not fourteen): gate/up 14.7 -> 14.2 us on MI355X
-      // against fourteen-wave workgroups, two per CU (one A/B run, same outputs).
-      if (112 % (a.K >> 7) == 0) return launch_m1<7, 2, 16>(a, st, M1Fuse{}, 4);
-      return launch_m1<14, 2, 16>(a, st);
+    M1Layout L;
+    const hipError_t e = m1_layout(a.N, a.K, &L);
+    if (e != hipSuccess) return e;
+    M1Fuse fz;
+    fz.rows = L.rows;
+    fz.xfirst = L.xfirst;
+    if (L.gr == 0) {
+      if (L.nw == 14) return launch_m1<14, 2, 0>(a, st, fz, L.wpc);
+      return launch_m1<16, 2, 0>(a, st, fz, L.wpc);
     }
-    // Eight-wave plans run with seven waves when 16 x 7 is a multiple of K / 128 (e.g. the qkv
-    // and o shapes, K / 128 = 28): each lane then meets one k-group only and keeps its
-    // activation fragments in registers (qkv 5.26 -> 5.15 us, o 4.72 -> 4.55 on MI355X; same
+    if (L.nw == 16) return launch_m1<16, 2, 16>(a, st, fz, L.wpc);
+    // seven-wave workgroups, four per CU, for gate/up: each lane keeps its activation
+    // fragments in registers, and a group barrier waits for seven waves, not fourteen (gate/up
+    // 14.7 -> 14.2 us on MI355X against fourteen-wave workgroups, two per CU; same outputs)
+    if (L.nw == 7) return launch_m1<7, 2, 16>(a, st, fz, L.wpc);
+    if (L.nw == 14) return launch_m1<14, 2, 16>(a, st, fz, L.wpc);
+    // Eight-wave plans run with seven waves when 16 x 7 is a multiple of K / 128: each lane
+    // then meets one k-group only and keeps its activation fragments in registers (same
     // outputs). The fused decode entries keep eight waves (their activation staging needs one
     // vector per thread).
     const bool fc7 = 112 % (a.K >> 7) == 0;
-    if (p.nw == 8 && p.rt == 2 && p.gr == 16) return fc7 ? launch_m1<7, 2, 16>(a, st) : launch_m1<8, 2, 16>(a, st);
-    if (p.nw == 8 && p.rt == 2 && p.gr == 8) return fc7 ? launch_m1<7, 2, 8>(a, st) : launch_m1<8, 2, 8>(a, st);
-    return hipErrorInvalidValue;
+    if (L.gr == 16) return fc7 ? launch_m1<7, 2, 16>(a, st, fz, L.wpc) : launch_m1<8, 2, 16>(a, st, fz, L.wpc);
+    return fc7 ? launch_m1<7, 2, 8>(a, st, fz, L.wpc) : launch_m1<8, 2, 8>(a, st, fz, L.wpc);
   }
   if (p.m8) {
     switch (p.rt) {
@@ -1502,60 +1563,94 @@ namespace {
 // The norm prologue keeps its vectors live across the row reduction, so it is compiled for
 // as few vectors per thread as the row needs (registers decide how many workgroups fit a CU).
 template <int NW, int GR, int YM, int XV>
-hipError_t launch_m1_norm(const GemvArgs& a, const M1Fuse& fz, hipStream_t st) {
-  if (fz.radd) return launch_m1<NW, 2, GR, kXNormAdd, YM, XV>(a, st, fz);
-  return launch_m1<NW, 2, GR, kXNorm, YM, XV>(a, st, fz);
+hipError_t launch_m1_norm(const GemvArgs& a, const M1Fuse& fz, hipStream_t st, int wpc) {
+  if (fz.radd) return launch_m1<NW, 2, GR, kXNormAdd, YM, XV>(a, st, fz, wpc);
+  return launch_m1<NW, 2, GR, kXNorm, YM, XV>(a, st, fz, wpc);
 }
 
 template <int NW, int GR, int YM>
-hipError_t launch_m1_x(const GemvArgs& a, const M1Fuse& fz, bool norm, hipStream_t st) {
-  if (!norm) return launch_m1<NW, 2, GR, kXPlain, YM>(a, st, fz);
+hipError_t launch_m1_x(const GemvArgs& a, const M1Fuse& fz, bool norm, hipStream_t st, int wpc) {
+  if (!norm) return launch_m1<NW, 2, GR, kXPlain, YM>(a, st, fz, wpc);
   const int C = a.K >> 7, nvec = 16 * ((C + 15) & ~15);
-  if (nvec <= NW * kWave) return launch_m1_norm<NW, GR, YM, 1>(a, fz, st);
-  if (nvec <= 2 * NW * kWave) return launch_m1_norm<NW, GR, YM, 2>(a, fz, st);
-  return launch_m1_norm<NW, GR, YM, 4>(a, fz, st);
+  if (nvec <= NW * kWave) return launch_m1_norm<NW, GR, YM, 1>(a, fz, st, wpc);
+  if (nvec <= 2 * NW * kWave) return launch_m1_norm<NW, GR, YM, 2>(a, fz, st, wpc);
+  return launch_m1_norm<NW, GR, YM, 4>(a, fz, st, wpc);
 }
 
 template <int NW, int GR>
 hipError_t launch_m1_fused(const GemvArgs& a, const M1Fuse& fz, bool norm, bool swiglu,
-                           hipStream_t st) {
-  if (swiglu) return launch_m1_x<NW, GR, kYSwiglu>(a, fz, norm, st);
-  return launch_m1_x<NW, GR, kYPlain>(a, fz, norm, st);
+                           hipStream_t st, int wpc) {
+  if (swiglu) return launch_m1_x<NW, GR, kYSwiglu>(a, fz, norm, st, wpc);
+  return launch_m1_x<NW, GR, kYPlain>(a, fz, norm, st, wpc);
 }
 
 }  // namespace
 
-hipError_t launch_gemv_attn(const GemvArgs& a, const GemvPlan& p, const M1Fuse& fz,
+hipError_t launch_gemv_attn(const GemvArgs& a, const GemvPlan& p, const M1Fuse& fz0,
                             hipStream_t st, int* reject) {
   *reject = 0;
   const int C = a.K >> 7, CP = (C + 15) & ~15;
-  if (!p.m1 || p.rt != 2 || 16 * CP > p.nw * kWave) {
+  if (!p.m1 || p.rt != 2) {
     *reject = 1;
     return hipSuccess;
   }
-  if (p.nw == 16 && p.gr == 16) return launch_m1<16, 2, 16, kXAttn, kYPlain, 1>(a, st, fz);
-  if (p.nw == 14 && p.gr == 16) return launch_m1<14, 2, 16, kXAttn, kYPlain, 1>(a, st, fz);
-  if (p.nw == 8 && p.gr == 16) return launch_m1<8, 2, 16, kXAttn, kYPlain, 1>(a, st, fz);
-  if (p.nw == 8 && p.gr == 8) return launch_m1<8, 2, 8, kXAttn, kYPlain, 1>(a, st, fz);
+  M1Layout L;
+  const hipError_t e = m1_layout(a.N, a.K, &L);
+  if (e != hipSuccess) return e;
+  // the plain plan's seven-wave workgroups: fourteen here (one activation vector per thread)
+  const int nw = L.nw == 7 ? 14 : L.nw;
+  if (L.nw == 7) L.wpc = 2;
+  if (16 * CP > nw * kWave) {
+    *reject = 1;
+    return hipSuccess;
+  }
+  M1Fuse fz = fz0;
+  fz.rows = L.rows;
+  fz.xfirst = L.xfirst;
+  if (L.gr == 0) {
+    if (nw == 14) return launch_m1<14, 2, 0, kXAttn, kYPlain, 1>(a, st, fz, L.wpc);
+    return launch_m1<16, 2, 0, kXAttn, kYPlain, 1>(a, st, fz, L.wpc);
+  }
+  if (nw == 16 && L.gr == 16) return launch_m1<16, 2, 16, kXAttn, kYPlain, 1>(a, st, fz, L.wpc);
+  if (nw == 14 && L.gr == 16) return launch_m1<14, 2, 16, kXAttn, kYPlain, 1>(a, st, fz, L.wpc);
+  if (nw == 8 && L.gr == 16) return launch_m1<8, 2, 16, kXAttn, kYPlain, 1>(a, st, fz, L.wpc);
+  if (nw == 8 && L.gr == 8) return launch_m1<8, 2, 8, kXAttn, kYPlain, 1>(a, st, fz, L.wpc);
   *reject = 1;
   return hipSuccess;
 }
 
-hipError_t launch_gemv_fused(const GemvArgs& a, const GemvPlan& p, const M1Fuse& fz, bool norm,
+hipError_t launch_gemv_fused(const GemvArgs& a, const GemvPlan& p, const M1Fuse& fz0, bool norm,
                              bool swiglu, hipStream_t st, int* reject) {
   *reject = 0;
   const int C = a.K >> 7, CP = (C + 15) & ~15;
-  if (!p.m1 || p.rt != 2 || (swiglu && a.N % 16) ||
-      (norm && 16 * CP > kXVecs * p.nw * kWave)) {
+  if (!p.m1 || p.rt != 2 || (swiglu && a.N % 16)) {
     *reject = 1;
     return hipSuccess;
   }
-  // the SwiGLU pairing needs 16-row groups
-  const int gr = swiglu ? 16 : p.gr;
-  if (p.nw == 16 && gr == 16) return launch_m1_fused<16, 16>(a, fz, norm, swiglu, st);
-  if (p.nw == 14 && gr == 16) return launch_m1_fused<14, 16>(a, fz, norm, swiglu, st);
-  if (p.nw == 8 && gr == 16) return launch_m1_fused<8, 16>(a, fz, norm, swiglu, st);
-  if (p.nw == 8 && gr == 8 && !swiglu) return launch_m1_x<8, 8, kYPlain>(a, fz, norm, st);
+  M1Layout L;
+  const hipError_t e = m1_layout(a.N, a.K, &L);
+  if (e != hipSuccess) return e;
+  // the SwiGLU pairing needs 16-row groups; the plain plan's seven-wave workgroups run with
+  // fourteen waves, two per CU (the decode step measured 1.511 against 1.458 ms per token
+  // with seven-wave fused GEMVs)
+  if (swiglu && L.gr != 16) L = M1Layout{L.nw == 16 ? 16 : 8, 16, 0, 2, false};
+  const int nw = L.nw == 7 ? 14 : L.nw;
+  if (L.nw == 7) L.wpc = 2;
+  if (norm && 16 * CP > kXVecs * nw * kWave) {
+    *reject = 1;
+    return hipSuccess;
+  }
+  M1Fuse fz = fz0;
+  fz.rows = L.rows;
+  fz.xfirst = L.xfirst;
+  if (L.gr == 0) {
+    if (nw == 14) return launch_m1_x<14, 0, kYPlain>(a, fz, norm, st, L.wpc);
+    return launch_m1_x<16, 0, kYPlain>(a, fz, norm, st, L.wpc);
+  }
+  if (nw == 16 && L.gr == 16) return launch_m1_fused<16, 16>(a, fz, norm, swiglu, st, L.wpc);
+  if (nw == 14 && L.gr == 16) return launch_m1_fused<14, 16>(a, fz, norm, swiglu, st, L.wpc);
+  if (nw == 8 && L.gr == 16) return launch_m1_fused<8, 16>(a, fz, norm, swiglu, st, L.wpc);
+  if (nw == 8 && L.gr == 8 && !swiglu) return launch_m1_x<8, 8, kYPlain>(a, fz, norm, st, L.wpc);
   *reject = 1;
   return hipSuccess;
 }

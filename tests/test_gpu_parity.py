@@ -142,6 +142,19 @@ def test_gemv_m1_kgroup_counts(kernels, oracle, N, K):
     check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
 
 
+@pytest.mark.parametrize("N,K", [(4608, 3584), (3584, 3584), (4100, 3584), (4609, 3584), (257, 2560),
+                                 (5000, 1024), (8960, 1536), (255, 256)])
+def test_gemv_m1_one_round_groups(kernels, oracle, N, K):
+    """M = 1 shapes small enough for one workgroup per CU with ceil(N / CUs) rows each: row
+    groups whose pieces end inside a 1 KiB block (the last block partly another group's), a last
+    group shorter than the rest (N tails), and (4609, 3584) just past the one-round limit."""
+    G = 128
+    Wq, S = synth.weights(N, K, G, seed=N * 3 + K)
+    X = synth.activations(1, K, seed=N + 11)
+    y = run_linear(kernels, X, Wq, S, G)
+    check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
+
+
 @pytest.mark.parametrize("M", [2, 5, 8])
 @pytest.mark.parametrize("N,K", [(24, 256), (200, 4096), (136, 4352), (72, 12288), (40, 16384),
                                  (24, 18944), (9, 20480)])
