@@ -414,7 +414,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
 //  * Branch-free inner loop: the per-chunk offsets are stored four times (one 16-byte LDS read
 //    initialises the whole MFMA accumulator), the diagonal value is picked with three selects,
 //    and lanes off the diagonal (or on a padded slot) write to a private dummy slot.
-template <int NW, int R, int GR, int XM, int YM, int XV, bool FC>
+template <int NW, int R, int GR, int XM, int YM, int XV, bool FC, bool XF>
 __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
     const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int N, int K, M1Fuse fz) {
@@ -470,8 +470,16 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, 16u * e, 0, 0));
   };
   u32x4_t xa[XV], xb[XV], xw[XV];
-  // attention merge: this thread's 8 dims (head e / 16) of the first kAttnBatch splits
-  constexpr int kAttnBatch = NW <= 8 ? 8 : 4;  // registers: fewer with more waves
+  // attention merge: this thread's 8 dims (head v / 16) of kAttnBatch splits per round (fewer
+  // with more waves: registers). One-round layouts (GR == 0: one workgroup of 14 or 16 waves per
+  // CU) with at least two threads per activation vector split each round's splits over two
+  // halves of the threads (thread t < KV and thread t + KV, same dims), which combine through
+  // LDS, so a round covers 2 kAttnBatch splits with one load each.
+  constexpr int kAttnBatch = NW <= 8 ? 8 : 4;
+  const int ahalves = GR == 0 && NT >= 2 * KV ? 2 : 1;  // uniform
+  const int kAttnRound = kAttnBatch * ahalves;
+  const int ahf = ahalves == 2 && tid >= KV ? 1 : 0;  // which half of each round
+  const int av = tid - ahf * KV;                           // activation vector merged
   float2 aml[kAttnBatch];
   f32x4_t ao[kAttnBatch][2];
   int nsplit = 0;
@@ -487,30 +495,32 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     // the workspace read as zeros through the buffer range check.
     const int posv = __builtin_amdgcn_readfirstlane(*fz.pos);
     xa[0] = vec_load(vec_rsrc(X), tid);
-    const int hq = tid >> 4, d0 = 8 * (tid & 15);
+    const int hq = av >> 4, d0 = 8 * (av & 15);
     const int smax = (fz.max_len + kAttnDecodeChunk - 1) / kAttnDecodeChunk;
     const auto ores = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(fz.opart), (short)0,
                                                         smax * fz.heads * 128 * 4, 0x00020000);
     const auto mres = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(fz.ml), (short)0,
                                                         smax * fz.heads * 2 * 4, 0x00020000);
-    const bool tl = tid < KV;
+    const bool tl = av < KV && tid < ahalves * KV;
 #pragma unroll
-    for (int sp = 0; sp < kAttnBatch; ++sp) {
+    for (int sp0 = 0; sp0 < kAttnBatch; ++sp0) {
+      const int sp = ahf * kAttnBatch + sp0;
       const uint32_t oo = tl ? 4u * (uint32_t)((sp * fz.heads + hq) * 128 + d0) : kOOB;
       const uint32_t mo = tl ? 4u * (uint32_t)((sp * fz.heads + hq) * 2) : kOOB;
-      ao[sp][0] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ores, oo, 0, 0));
-      ao[sp][1] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ores, oo + 16u, 0, 0));
+      ao[sp0][0] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ores, oo, 0, 0));
+      ao[sp0][1] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ores, oo + 16u, 0, 0));
       const auto m2 = __builtin_amdgcn_raw_buffer_load_b64(mres, mo, 0, 0);
-      aml[sp] = make_float2(__builtin_bit_cast(float, (uint32_t)m2[0]),
-                            __builtin_bit_cast(float, (uint32_t)m2[1]));
+      aml[sp0] = make_float2(__builtin_bit_cast(float, (uint32_t)m2[0]),
+                             __builtin_bit_cast(float, (uint32_t)m2[1]));
     }
     const int n = min(posv + 1, fz.max_len);
     nsplit = n > 0 ? (n + kAttnDecodeChunk - 1) / kAttnDecodeChunk : 0;
 #pragma unroll
-    for (int sp = 0; sp < kAttnBatch; ++sp) {
+    for (int sp0 = 0; sp0 < kAttnBatch; ++sp0) {
+      const int sp = ahf * kAttnBatch + sp0;
       if (!(nsplit > 1 && sp < nsplit && tl)) {  // masked after the load (no branch around it)
-        aml[sp] = make_float2(-INFINITY, 0.f);
-        ao[sp][0] = ao[sp][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        aml[sp0] = make_float2(-INFINITY, 0.f);
+        ao[sp0][0] = ao[sp0][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     }
   } else {
@@ -531,7 +541,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   uint32_t rsc[R];
   // (one workgroup per CU) the vector memory pipeline returns loads in issue order, so the
   // activation, issued by every wave before this barrier, does not wait for weight blocks
-  if (fz.xfirst) __builtin_amdgcn_s_barrier();
+  if constexpr (XF) __builtin_amdgcn_s_barrier();
 #pragma unroll
   for (int u = 0; u < R; ++u) issue(ring[u], rsc[u]);
   __builtin_amdgcn_sched_barrier(0);
@@ -562,16 +572,17 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     // (base-2 logits), sum, divide once
     u32x4_t xv = xa[0];
     if (nsplit > 1) {
-      const int hq = tid >> 4, d0 = 8 * (tid & 15);
+      const int hq = av >> 4, d0 = 8 * (av & 15);
       float m = -INFINITY, l = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int s0 = 0; s0 < nsplit; s0 += kAttnBatch) {
-        if (s0 > 0) {  // later batches (contexts beyond 4 splits)
+      for (int s0 = 0; s0 < nsplit; s0 += kAttnRound) {
+        if (s0 > 0) {  // later rounds (contexts beyond one round of splits)
 #pragma unroll
           for (int sp = 0; sp < kAttnBatch; ++sp) {
             aml[sp] = make_float2(-INFINITY, 0.f);
             ao[sp][0] = ao[sp][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-            if (s0 + sp < nsplit && tid < KV) {
-              const size_t row = (size_t)(s0 + sp) * fz.heads + hq;
+            const int spl = s0 + ahf * kAttnBatch + sp;
+            if (spl < nsplit && av < KV && tid < ahalves * KV) {
+              const size_t row = (size_t)spl * fz.heads + hq;
               aml[sp] = *reinterpret_cast<const float2*>(&fz.ml[row * 2]);
               const f32x4_t* src = reinterpret_cast<const f32x4_t*>(&fz.opart[row * 128 + d0]);
               ao[sp][0] = src[0];
@@ -591,6 +602,30 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
             acc[4 + q] = acc[4 + q] * fo + ao[sp][1][q] * fs;
           }
           m = mn;
+        }
+      }
+      if (ahalves == 2) {
+        // the second half's (max, sum, output) through LDS (after the partial table), combined
+        // by the first half as one more split
+        float* xch = part + 2 * NP + 64 + 12 * av;
+        if (ahf == 1 && av < KV) {
+          *reinterpret_cast<f32x4_t*>(xch) = f32x4_t{m, l, 0.f, 0.f};
+          *reinterpret_cast<f32x4_t*>(xch + 4) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
+          *reinterpret_cast<f32x4_t*>(xch + 8) = f32x4_t{acc[4], acc[5], acc[6], acc[7]};
+        }
+        __syncthreads();
+        if (ahf == 0 && av < KV) {
+          const f32x4_t ml1 = *reinterpret_cast<const f32x4_t*>(xch);
+          const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(xch + 4);
+          const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(xch + 8);
+          const float mn = fmaxf(m, ml1[0]);  // finite: split 0 is in the first half
+          const float fo = exp2f(m - mn), fs = exp2f(ml1[0] - mn);
+          l = l * fo + ml1[1] * fs;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            acc[q] = acc[q] * fo + a0[q] * fs;
+            acc[4 + q] = acc[4 + q] * fo + a1[q] * fs;
+          }
         }
       }
       const float il = 1.f / l;
@@ -693,7 +728,9 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
       float v = s1 ? t[1] : t[0];
       v = s2 ? t[2] : v;
       v = s3 ? t[3] : v;
-      float* dst = diag && 16 * b + j < NP ? pt + 16 * b : dummy;
+      // (groups of a multiple of 16 rows always end on a block boundary)
+      const bool in_group = GR > 0 && GR % 16 == 0 ? b < NBG : 16 * b + j < NP;
+      float* dst = diag && in_group ? pt + 16 * b : dummy;
       *dst = __uint_as_float(rsc[u] << 16) * v;  // the 16-bit load zero-extends
       if constexpr (!decltype(fixed)::value) {
         c += c_step;
@@ -750,9 +787,12 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
   }
 }
 
-size_t m1_bytes(int K, int gr) {
+// Dynamic LDS of w4_gemv_m1_kernel: the staged activation, the offsets, the double-buffered
+// partial table with its dummy slots and, for the two-half attention merge, its exchange area.
+size_t m1_bytes(int K, int gr, bool attn_halves = false) {
   const int C = K >> 7, CP = (C + 15) & ~15;
-  return (size_t)CP * 136 * 2 + (size_t)CP * 16 + (size_t)(2 * gr * C + 64) * 4;
+  return (size_t)CP * 136 * 2 + (size_t)CP * 16 + (size_t)(2 * gr * C + 64) * 4 +
+         (attn_halves ? (size_t)(K >> 3) * 12 * 4 : 0);
 }
 
 
@@ -1249,16 +1289,16 @@ hipError_t launch_xlds(const GemvArgs& a, hipStream_t st) {
   return hipSuccess;
 }
 
-template <int NW, int R, int GR, int XM, int YM, int XV, bool FC>
+template <int NW, int R, int GR, int XM, int YM, int XV, bool FC, bool XF>
 hipError_t launch_m1_fc(const GemvArgs& a, hipStream_t st, const M1Fuse& fz, int wpc) {
-  const void* fn = reinterpret_cast<const void*>(&w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV, FC>);
+  const void* fn = reinterpret_cast<const void*>(&w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV, FC, XF>);
   // the planner keeps the dynamic part under 96 KiB; the limit leaves room for static LDS
   static const hipError_t attr =
       hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
   if (attr != hipSuccess) return attr;
   const int rows = GR > 0 ? GR : fz.rows;
   if (rows <= 0) return hipErrorInvalidValue;
-  const size_t lds = m1_bytes(a.K, rows);
+  const size_t lds = m1_bytes(a.K, rows, XM == kXAttn && GR == 0);
   int per_cu = 0;
   hipError_t e = cached_occupancy(fn, NW * kWave, lds, &per_cu);
   if (e != hipSuccess) return e;
@@ -1269,15 +1309,24 @@ hipError_t launch_m1_fc(const GemvArgs& a, hipStream_t st, const M1Fuse& fz, int
   // lengthen the memory queues.
   const int ngroups = (a.N + rows - 1) / rows;
   const int grid = max(1, min(ngroups, min(max(per_cu, 1), wpc) * cus));
-  hipLaunchKernelGGL((w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV, FC>), dim3(grid), dim3(NW * kWave), lds,
+  hipLaunchKernelGGL((w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV, FC, XF>), dim3(grid), dim3(NW * kWave), lds,
                      st, a.X, a.Wq, a.S, a.Y, a.N, a.K, fz);
   return hipSuccess;
 }
 
+// FC when 16 NW is a multiple of K / 128; the activation-first barrier (XF) when the layout asks
+// for it, compiled only for the layouts that can hold one workgroup per CU.
 template <int NW, int R, int GR, int XM = kXPlain, int YM = kYPlain, int XV = kXVecs>
 hipError_t launch_m1(const GemvArgs& a, hipStream_t st, const M1Fuse& fz = M1Fuse{}, int wpc = 2) {
-  if ((16 * NW) % (a.K >> 7) == 0) return launch_m1_fc<NW, R, GR, XM, YM, XV, true>(a, st, fz, wpc);
-  return launch_m1_fc<NW, R, GR, XM, YM, XV, false>(a, st, fz, wpc);
+  const bool fc = (16 * NW) % (a.K >> 7) == 0;
+  if constexpr (GR == 0 || (NW == 16 && GR == 16)) {
+    if (fz.xfirst) {
+      if (fc) return launch_m1_fc<NW, R, GR, XM, YM, XV, true, true>(a, st, fz, wpc);
+      return launch_m1_fc<NW, R, GR, XM, YM, XV, false, true>(a, st, fz, wpc);
+    }
+  }
+  if (fc) return launch_m1_fc<NW, R, GR, XM, YM, XV, true, false>(a, st, fz, wpc);
+  return launch_m1_fc<NW, R, GR, XM, YM, XV, false, false>(a, st, fz, wpc);
 }
 
 // Workgroups per CU the M = 2..8 kernel can hold (occupancy), or a negative error.
@@ -1606,8 +1655,14 @@ hipError_t launch_gemv_attn(const GemvArgs& a, const GemvPlan& p, const M1Fuse& 
   }
   M1Fuse fz = fz0;
   fz.rows = L.rows;
-  fz.xfirst = L.xfirst;
+  // no activation-first barrier here: each workgroup reads every split's partials (115 KB at
+  // 28 heads and 8 splits), and the weight stream should not queue behind them
+  fz.xfirst = 0;
   if (L.gr == 0) {
+    // eight waves with four blocks each (one round of up to 32 blocks, as the plain layout's
+    // 14 or 16 waves with two): every thread then merges all splits of a round itself
+    if ((L.rows * C + 15) / 16 <= 32 && 16 * CP <= 8 * kWave)
+      return launch_m1<8, 4, 0, kXAttn, kYPlain, 1>(a, st, fz, L.wpc);
     if (nw == 14) return launch_m1<14, 2, 0, kXAttn, kYPlain, 1>(a, st, fz, L.wpc);
     return launch_m1<16, 2, 0, kXAttn, kYPlain, 1>(a, st, fz, L.wpc);
   }

@@ -58,9 +58,10 @@ struct M1Fuse {
   int heads = 0;
   // launch layout (set by the launcher, not by the fused operators):
   int rows = 0;    // rows per group when the kernel's GR template argument is 0
-  int xfirst = 0;  // every wave issues its activation loads before any wave of the workgroup
-                   // issues weight loads (one workgroup per CU: the activation then does not
-                   // queue behind the weight stream in the CU's memory pipeline)
+  int xfirst = 0;  // (read by the launcher, which compiles it in) every wave issues its
+                   // activation loads before any wave of the workgroup issues weight loads (one
+                   // workgroup per CU: the activation then does not queue behind the weight
+                   // stream in the CU's memory pipeline)
 };
 hipError_t launch_gemv_attn(const GemvArgs& a, const GemvPlan& p, const M1Fuse& fz,
                             hipStream_t st, int* reject);
