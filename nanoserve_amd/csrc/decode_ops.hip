@@ -368,6 +368,12 @@ __global__ void __launch_bounds__(kAttnBlock)
     a1 = ld16(qres, o0 == kOOB ? kOOB : o0 + 16u);
     b0 = b1 = u32x4_t{};
   }
+  // Every wave's q / bias / angle loads are issued before any wave issues its cache rows: the
+  // CU's vector memory path returns data in issue order, so otherwise the q of the later waves
+  // waits behind the earlier waves' cache rows (and q is needed first).
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
   const uint32_t head_bytes = (uint32_t)max_len * D * 2;
   const auto kres = __builtin_amdgcn_make_buffer_rsrc(kc + (size_t)g * max_len * D, (short)0,
                                                       (int)head_bytes, 0x00020000);
@@ -424,7 +430,7 @@ __global__ void __launch_bounds__(kAttnBlock)
       *reinterpret_cast<u32x4_t*>(&qb[h][16 * cc]) = u32x4_t{};
       *reinterpret_cast<u32x4_t*>(&qb[h][16 * cc + 8]) = u32x4_t{};
     }
-    if (!tab) __syncthreads();  // the angles in LDS (uniform branch; the q slots are read after
+    if (!tab) lds_sync();  // the angles in LDS (uniform branch; the q slots are read after
                                 // the next barrier)
     if (is_q || is_k) {
       float lo[8], hi[8];
@@ -484,7 +490,7 @@ __global__ void __launch_bounds__(kAttnBlock)
       *reinterpret_cast<u32x4_t*>(&qb[h][16 * cc + 8]) = a1;
     }
   }
-  __syncthreads();
+  lds_sync();
   // the token's own row comes from LDS; its value row is swapped in where the value loop
   // reads vv (a substitution here would make every value load complete first)
   int inew = -1;
@@ -520,7 +526,7 @@ __global__ void __launch_bounds__(kAttnBlock)
   m = fmaxf(m, lane_xor16(m));
   m = fmaxf(m, lane_xor32(m));
   if (grp == 0) red_m[w][h] = m;
-  __syncthreads();
+  lds_sync();
   m = red_m[0][h];
 #pragma unroll
   for (int i = 1; i < NWV; ++i) m = fmaxf(m, red_m[i][h]);
@@ -534,29 +540,34 @@ __global__ void __launch_bounds__(kAttnBlock)
   l += lane_xor16(l);
   l += lane_xor32(l);
   if (grp == 0) red_l[w][h] = l;
-  __syncthreads();
+  lds_sync();
 
-  // ---- values: lane owns dim D/2 dh + lane
+  // ---- values: lane owns dim D/2 dh + lane. The wave's 16 probability rows (8 heads each, the
+  // same LDS words for every lane) are all read before the first product, so the reads overlap
+  // instead of costing one LDS round trip per row; rows past the position take a zero value
+  // (their probability is 0 as well), so the loop has no branch.
+  f32x4_t pr[16][2];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    pr[i][0] = *reinterpret_cast<const f32x4_t*>(&ps[16 * w + i][0]);
+    pr[i][1] = *reinterpret_cast<const f32x4_t*>(&ps[16 * w + i][4]);
+  }
   float acc[RP];
 #pragma unroll
   for (int hh = 0; hh < RP; ++hh) acc[hh] = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    if (i < rows) {
-      const uint32_t vi = i == inew ? vnw : vv[i];
-      const float v0 = __uint_as_float(vi << 16);
-      const f32x4_t p0 = *reinterpret_cast<const f32x4_t*>(&ps[16 * w + i][0]);
-      const f32x4_t p1 = *reinterpret_cast<const f32x4_t*>(&ps[16 * w + i][4]);
+    const uint32_t vi = i < rows ? (i == inew ? vnw : vv[i]) : 0u;
+    const float v0 = __uint_as_float(vi << 16);
 #pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        acc[hh] = fmaf(p0[hh], v0, acc[hh]);
-        acc[hh + 4] = fmaf(p1[hh], v0, acc[hh + 4]);
-      }
+    for (int hh = 0; hh < 4; ++hh) {
+      acc[hh] = fmaf(pr[i][0][hh], v0, acc[hh]);
+      acc[hh + 4] = fmaf(pr[i][1][hh], v0, acc[hh + 4]);
     }
   }
 #pragma unroll
   for (int hh = 0; hh < RP; ++hh) ored[w][hh][lane] = acc[hh];
-  __syncthreads();
+  lds_sync();
 
   const bool single = nsplit == 1;
   for (int i = tid; i < R * D / 2; i += kAttnBlock) {

@@ -29,17 +29,30 @@ constexpr int kStreamAux = 3;
 // activation load of the decode GEMV (w4_gemv.hip) reads the same split layout.
 constexpr int kAttnDecodeChunk = 128;
 
+// Workgroup barrier for LDS traffic: this wave's LDS operations complete (lgkmcnt(0)), then
+// s_barrier. Outstanding global loads and stores stay in flight; the release fence of
+// __syncthreads() would make a wave that has stored to global memory wait for every vector
+// memory operation it issued before (loads and stores share one in-order counter on gfx9).
+// The empty asm statements keep the compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_sync() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // gfx9 encoding: vmcnt 63, expcnt 7, lgkmcnt 0
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h16) {
   return __uint_as_float(h16 << 16);
 }
 
 // fp32 -> bf16 bits, round to nearest even, NaN kept quiet (the reference's
-// __float2bfloat16 / __floats2bfloat162_rn semantics, kernels/fused/vec.cuh:14-19).
+// __float2bfloat16 / __floats2bfloat162_rn semantics, kernels/fused/vec.cuh:14-19). Written as
+// a select, not an early return: the compiler turns the early-return form into a divergent
+// branch (exec-mask save and restore) around every conversion.
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (u & 0x7fffffffu) > 0x7f800000u ? (u >> 16) | 0x40u : r;
 }
 
 // Two fp32 -> packed bf16x2 (lo in bits 0..15), RNE. An fp32 -> bf16 vector truncation, which
@@ -84,8 +97,11 @@ __device__ __forceinline__ u32x4_t pack8(const float (&f)[8]) {
   return u;
 }
 
+// fp32 rounded to the nearest bf16 (ties to even), as an fp32: the hardware conversion
+// (v_cvt_pk_bf16_f32, one instruction) and a shift, where the integer form takes six
+// instructions. The same rounding as f32_to_bf16_rne for every non-NaN input.
 __device__ __forceinline__ float round_bf16(float f) {
-  return bf16_bits_to_f32(f32_to_bf16_rne(f));
+  return bf16_bits_to_f32(pack_bf16x2_rne(f, 0.f));
 }
 
 // The value of lane l ^ 32 and of lane l ^ 16, by the gfx950 lane-swap instructions (no LDS
