@@ -291,7 +291,6 @@ __global__ void __launch_bounds__(kAttnBlock)
   constexpr int NWV = kAttnWaves;
   constexpr int QS = D + 8;  // padded q row (bf16 elements)
   __shared__ __attribute__((aligned(16))) uint16_t qb[16][QS];
-  __shared__ __attribute__((aligned(16))) float ps[kChunk][RP];
   __shared__ float red_m[NWV][16];
   __shared__ float red_l[NWV][16];
   __shared__ float ored[NWV][RP][D / 2];
@@ -383,11 +382,15 @@ __global__ void __launch_bounds__(kAttnBlock)
   const uint32_t krow_off = (uint32_t)(start + krow) * D * 2 + 16u * grp;
 #pragma unroll
   for (int s4 = 0; s4 < 4; ++s4) ka[s4] = ld16(kres, krow_off + 64u * s4);
-  const uint32_t vrow_off = (uint32_t)(start + 16 * w) * D * 2 + 2u * (D / 2 * dh + lane);
+  // value rows in the MFMA B layout: lane l holds rows 4 (l / 16) + t (t < 4) of the wave's 16
+  // at dims D/2 dh + 16 j + l % 16 (j < 4), one 2-byte load each: vv[4 j + t]
+  const uint32_t vrow_off =
+      (uint32_t)(start + 16 * w + 4 * grp) * D * 2 + 2u * (D / 2 * dh + r16);
   uint32_t vv[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i)
-    vv[i] = __builtin_amdgcn_raw_buffer_load_b16(vres, vrow_off + (uint32_t)i * D * 2, 0, 0);
+  for (int jt = 0; jt < 16; ++jt)
+    vv[jt] = __builtin_amdgcn_raw_buffer_load_b16(
+        vres, vrow_off + (uint32_t)(jt & 3) * D * 2 + 32u * (uint32_t)(jt >> 2), 0, 0);
 
   // ---- the position
   const int n = min(pos + 1, max_len);
@@ -491,18 +494,19 @@ __global__ void __launch_bounds__(kAttnBlock)
     }
   }
   lds_sync();
-  // the token's own row comes from LDS; its value row is swapped in where the value loop
-  // reads vv (a substitution here would make every value load complete first)
+  // the token's own row comes from LDS; its value row is swapped in where the value operands
+  // are built (a substitution here would make every value load complete first)
   int inew = -1;
-  uint32_t vnw = 0u;
+  uint32_t vnw[4] = {0u, 0u, 0u, 0u};
   if (has_new) {
     if (k_is_new) {
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4)
         ka[s4] = *reinterpret_cast<const u32x4_t*>(&knew[32 * s4 + 8 * grp]);
     }
-    inew = pos - start - 16 * w;
-    vnw = vnew[D / 2 * dh + lane];
+    inew = pos - start - 16 * w - 4 * grp;  // its t in this lane's four rows, if there
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vnw[j] = vnew[D / 2 * dh + 16 * j + r16];
   }
 
   // ---- scores: S[row][head] for the wave's 16 rows and 16 head slots
@@ -513,7 +517,9 @@ __global__ void __launch_bounds__(kAttnBlock)
     sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ka[s4]),
                                                  __builtin_bit_cast(bf16x8_t, qf), sc, 0, 0, 0);
   }
-  // lane: head h = r16, rows 16w + 4 grp + r (base-2 logits)
+  // lane: head h = r16, rows 16w + 4 grp + r (base-2 logits). Each wave normalises against its
+  // own maximum; the waves are merged in the output reduction (flash-attention style), so the
+  // softmax needs no workgroup barrier.
   const int h = r16;
   float sr[4];
   float m = -INFINITY;
@@ -525,73 +531,77 @@ __global__ void __launch_bounds__(kAttnBlock)
   }
   m = fmaxf(m, lane_xor16(m));
   m = fmaxf(m, lane_xor32(m));
-  if (grp == 0) red_m[w][h] = m;
-  lds_sync();
-  m = red_m[0][h];
-#pragma unroll
-  for (int i = 1; i < NWV; ++i) m = fmaxf(m, red_m[i][h]);
+  const float mz = m == -INFINITY ? 0.f : m;  // a wave past the position: all p = 0
+  // fp32 probabilities as two bf16 MFMA operands, p = hi + lo to within 2^-16 of p: the
+  // products stay as exact as the fp32 loop they replace
   float l = 0.f;
+  float ph[4], pl[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const float p = exp2f(sr[r] - m);  // 0 for masked rows
+    const float p = exp2f(sr[r] - mz);  // 0 for masked rows
     l += p;
-    if (h < RP) ps[16 * w + 4 * grp + r][h] = p;
+    ph[r] = round_bf16(p);
+    pl[r] = p - ph[r];
   }
   l += lane_xor16(l);
   l += lane_xor32(l);
-  if (grp == 0) red_l[w][h] = l;
-  lds_sync();
-
-  // ---- values: lane owns dim D/2 dh + lane. The wave's 16 probability rows (8 heads each, the
-  // same LDS words for every lane) are all read before the first product, so the reads overlap
-  // instead of costing one LDS round trip per row; rows past the position take a zero value
-  // (their probability is 0 as well), so the loop has no branch.
-  f32x4_t pr[16][2];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    pr[i][0] = *reinterpret_cast<const f32x4_t*>(&ps[16 * w + i][0]);
-    pr[i][1] = *reinterpret_cast<const f32x4_t*>(&ps[16 * w + i][4]);
+  if (grp == 0) {
+    red_m[w][h] = m;
+    red_l[w][h] = l;
   }
-  float acc[RP];
+
+  // ---- values on the matrix cores: O[head][dim] = sum over the wave's 16 rows of P[head][row]
+  // V[row][dim]. v_mfma_f32_16x16x16_bf16: A = P (lane l: head l % 16, rows 4 (l / 16) + t,
+  // exactly the score layout), B = V (lane l: rows 4 (l / 16) + t, dim l % 16 of each 16-dim
+  // block j), D: lane l holds heads 4 (l / 16) + r of dim l % 16. Rows past the position get a
+  // zero value (their probability is 0 too; a zero also keeps stale cache words out).
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  const s16x4_t pah = __builtin_bit_cast(
+      s16x4_t, make_uint2(pack_bf16x2_rne(ph[0], ph[1]), pack_bf16x2_rne(ph[2], ph[3])));
+  const s16x4_t pal = __builtin_bit_cast(
+      s16x4_t, make_uint2(pack_bf16x2_rne(pl[0], pl[1]), pack_bf16x2_rne(pl[2], pl[3])));
+  f32x4_t ov[4];
 #pragma unroll
-  for (int hh = 0; hh < RP; ++hh) acc[hh] = 0.f;
+  for (int j = 0; j < 4; ++j) {
+    uint32_t e[4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const uint32_t vi = i < rows ? (i == inew ? vnw : vv[i]) : 0u;
-    const float v0 = __uint_as_float(vi << 16);
-#pragma unroll
-    for (int hh = 0; hh < 4; ++hh) {
-      acc[hh] = fmaf(pr[i][0][hh], v0, acc[hh]);
-      acc[hh + 4] = fmaf(pr[i][1][hh], v0, acc[hh + 4]);
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t v = t == inew ? vnw[j] : vv[4 * j + t];
+      e[t] = 4 * grp + t < rows ? v & 0xffffu : 0u;
     }
+    const s16x4_t vb = __builtin_bit_cast(s16x4_t, make_uint2(e[0] | (e[1] << 16), e[2] | (e[3] << 16)));
+    ov[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pah, vb, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+    ov[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pal, vb, ov[j], 0, 0, 0);
   }
 #pragma unroll
-  for (int hh = 0; hh < RP; ++hh) ored[w][hh][lane] = acc[hh];
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (4 * grp + r < RP) ored[w][4 * grp + r][16 * j + r16] = ov[j][r];
   lds_sync();
 
+  // ---- merge of the waves: each wave's output and sum rescaled from its maximum to the
+  // workgroup's (waves with no row in the position have maximum -inf and weight 0)
   const bool single = nsplit == 1;
   for (int i = tid; i < R * D / 2; i += kAttnBlock) {
     const int hh = i / (D / 2), d = D / 2 * dh + i % (D / 2);
-    float o = 0.f;
+    float mt = red_m[0][hh];
 #pragma unroll
-    for (int k = 0; k < NWV; ++k) o += ored[k][hh][d - D / 2 * dh];
+    for (int k = 1; k < NWV; ++k) mt = fmaxf(mt, red_m[k][hh]);
+    float o = 0.f, lt = 0.f;
+#pragma unroll
+    for (int k = 0; k < NWV; ++k) {
+      const float f = exp2f(red_m[k][hh] - mt);
+      o = fmaf(f, ored[k][hh][d - D / 2 * dh], o);
+      lt = fmaf(f, red_l[k][hh], lt);
+    }
     if (single) {
-      float lt = 0.f;
-#pragma unroll
-      for (int k = 0; k < NWV; ++k) lt += red_l[k][hh];
       out[(size_t)(g * R + hh) * D + d] = static_cast<uint16_t>(f32_to_bf16_rne(o / lt));
     } else {
       opart[((size_t)split * Hq + g * R + hh) * D + d] = o;
+      if (dh == 0 && d == 0)
+        *reinterpret_cast<float2*>(&ml[((size_t)split * Hq + g * R + hh) * 2]) = make_float2(mt, lt);
     }
-  }
-  if (!single && dh == 0 && tid < R) {
-    float mt = red_m[0][tid], lt = 0.f;
-#pragma unroll
-    for (int k = 0; k < NWV; ++k) {
-      mt = fmaxf(mt, red_m[k][tid]);
-      lt += red_l[k][tid];
-    }
-    *reinterpret_cast<float2*>(&ml[((size_t)split * Hq + g * R + tid) * 2]) = make_float2(mt, lt);
   }
 }
 
