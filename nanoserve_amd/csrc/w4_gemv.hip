@@ -751,11 +751,15 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     pass(std::integral_constant<bool, FC>{});
     __syncthreads();
     // 16-wave workgroups serve the long rows (the planner picks NW = 16 for C >= 64, e.g. down,
-    // C = 148): a wave per row, its lanes taking the row's partials c = lane, lane + 64, ...
-    // (one lane-wise pass, then a wave sum) instead of one wave walking C / 4 partials per lane
-    // for all the rows
-    constexpr bool kWideReduce = (NW == 16 || GR > 16 || GR == 0) && YM != kYSwiglu;
-    if constexpr (kWideReduce) {
+    // C = 148), and the one-round layouts (GR == 0) have every wave free at the end: a wave per
+    // row, its lanes taking the row's partials c = lane, lane + 64, ... (one lane-wise pass,
+    // then a wave sum) instead of one wave walking C / 4 partials per lane for all the rows.
+    // The order of additions per row depends only on which form runs, not on the group height,
+    // so the attention-merging launcher, which swaps one layout for another, sets fz.wide to
+    // keep the plain GEMV's bits.
+    constexpr bool kWideCT = YM != kYSwiglu && (NW == 16 || GR > 16 || GR == 0);
+    const bool wide = kWideCT || (XM == kXAttn && fz.wide != 0);
+    if (wide) {
       for (int rw = wv; rw < GRr; rw += NW) {
         const float* pr = part + (it & 1) * NP + rw * C;
         float v = 0.f;
@@ -767,7 +771,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
     } else if (wv == it % NW) {
       const float* pr = part + (it & 1) * NP;
       float v = 0.f;
-      if (j < GR)
+      if (j < GRr)
         for (int cc = kg; cc < C; cc += 4) v += pr[j * C + cc];
       v += lane_xor16(v);
       v += lane_xor32(v);
@@ -780,8 +784,8 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_m1_kernel(
         const int n = 8 * g + j;
         if (kg == 0 && j < 8 && 16 * g + j < N) Y[n] = (uint16_t)f32_to_bf16_rne(silu_mul(y, up));
       } else {
-        const int n = GR * g + j;
-        if (kg == 0 && j < GR && n < N) Y[n] = (uint16_t)f32_to_bf16_rne(v);
+        const int n = GRr * g + j;
+        if (kg == 0 && j < GRr && n < N) Y[n] = (uint16_t)f32_to_bf16_rne(v);
       }
     }
   }
@@ -1659,10 +1663,16 @@ hipError_t launch_gemv_attn(const GemvArgs& a, const GemvPlan& p, const M1Fuse& 
   // 28 heads and 8 splits), and the weight stream should not queue behind them
   fz.xfirst = 0;
   if (L.gr == 0) {
-    // eight waves with four blocks each (one round of up to 32 blocks, as the plain layout's
-    // 14 or 16 waves with two): every thread then merges all splits of a round itself
-    if ((L.rows * C + 15) / 16 <= 32 && 16 * CP <= 8 * kWave)
-      return launch_m1<8, 4, 0, kXAttn, kYPlain, 1>(a, st, fz, L.wpc);
+    // Where the plain layout is one round with up to 16 rows per CU (the o projection), the
+    // attention-merging GEMV runs eight-wave workgroups of 16-row groups, two per CU: every
+    // workgroup merges all the splits' partials (115 KB at 28 heads and 8 splits), and this
+    // layout's weight stream overlaps that better (decode step 1.385 -> 1.364 ms per token on
+    // MI355X against the one-round layout with eight waves of four blocks, one interleaved
+    // run). Both sum each row's partials in the same order: the same bits as the plain GEMV.
+    if (L.rows <= 16 && 16 * CP <= 8 * kWave) {
+      fz.wide = 1;  // the one-round layout's reduction form
+      return launch_m1<8, 2, 16, kXAttn, kYPlain, 1>(a, st, fz, 2);
+    }
     if (nw == 14) return launch_m1<14, 2, 0, kXAttn, kYPlain, 1>(a, st, fz, L.wpc);
     return launch_m1<16, 2, 0, kXAttn, kYPlain, 1>(a, st, fz, L.wpc);
   }

@@ -58,6 +58,8 @@ struct M1Fuse {
   int heads = 0;
   // launch layout (set by the launcher, not by the fused operators):
   int rows = 0;    // rows per group when the kernel's GR template argument is 0
+  int wide = 0;    // the group's rows are reduced a wave per row (the form the one-round
+                   // layouts take), for a launcher that runs another layout in their place
   int xfirst = 0;  // (read by the launcher, which compiles it in) every wave issues its
                    // activation loads before any wave of the workgroup issues weight loads (one
                    // workgroup per CU: the activation then does not queue behind the weight
