@@ -1095,6 +1095,17 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
   u32x4_t ring[R];
   uint32_t rsc[R];
   int g = blockIdx.x;
+  // With up to three pairs per wave, every wave issues its activation loads before any wave of
+  // the workgroup issues weight loads (the CU returns loads in issue order, so a later wave's
+  // activation would otherwise wait behind the earlier waves' weight blocks): on MI355X at M = 8
+  // o 5.61 -> 5.20 us, qkv 7.06 -> 6.90, gate/up 17.60 -> 17.47. With four or five pairs (down,
+  // 300 KB of activation per workgroup) the weights wait longer than the activation gains
+  // (18.88 -> 19.27 us), so those keep the interleaved order (one interleaved run each).
+  if constexpr (CW <= 3) {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  }
 #pragma unroll
   for (int i = 0; i < R; ++i) issue(ring[i], rsc[i], g, i);
   __builtin_amdgcn_sched_barrier(0);
