@@ -3,23 +3,24 @@
 // Replaces w4a16_gemv_kernel / w4a16_gemv (kernels/quant/w4a16.cuh:34-115 in the reference):
 //   Y[M][N] (bf16, RNE) = X[M][K] (bf16) . deq(Wq, S)^T, fp32 accumulation.
 //
-// Design (fast path, K % 128 == 0 and G % 128 == 0):
-//  * A wavefront owns a 16-row tile of W (RT tiles) and a contiguous range of 128-k chunks;
-//    the NW wavefronts of a workgroup split K (split-K inside the workgroup) and are reduced
-//    through LDS at the end.
-//  * Lane l = 16 h + r streams one 16-byte load of row r (words 4h..4h+3 of the chunk) per
-//    chunk: the whole wave reads 1 KiB of packed weights per chunk per tile.
-//  * The products run on the matrix cores: v_mfma_f32_16x16x32_bf16 with A = weights
-//    (row i = output feature), B = X^T (column j = batch row, padded to 16). The weight operand
-//    is the exact integer 128 + q in bf16 (0x4300 | q: one byte permute and one AND-OR per two
-//    weights, no float arithmetic); a second MFMA with the constant -136 per chunk removes the
-//    offset, so the chunk partial is sum_k x * (q - 8) exactly as the reference's integer
-//    dequant, and the bf16 group scale is applied in fp32 after the chunk. No weight is ever
-//    rounded: the dequant is exact, as in the reference GEMV (w4a16.cuh:28-32).
-//  * Loads of W and X are issued in batches of UB chunks, so each wave has up to UB x RT KiB
-//    of HBM reads in flight; several waves per SIMD overlap one another's batches.
-//  * Scales for the workgroup's rows are staged once in LDS, transposed to [group][row] so a
-//    lane reads its four rows' scales with one 8-byte LDS read.
+// Every fast-path kernel (K % 128 == 0, G % 128 == 0) shares one arithmetic: the weight operand
+// of v_mfma_f32_16x16x32_bf16 is the exact integer 128 + q in bf16 (0x4300 | q: bit operations,
+// no float arithmetic), the accumulator starts at -136 * sum_k x over the chunk (one MFMA
+// against a constant), so a chunk's partial is sum_k x * (q - 8) exactly, and the bf16 group
+// scale is applied in fp32 after the chunk. No weight is ever rounded: the dequant is exact, as
+// in the reference GEMV (w4a16.cuh:28-32). The kernels differ in how HBM is streamed:
+//  * w4_gemv_m1_kernel (M = 1, G = 128): the weights as one sequential stream of 1 KiB blocks
+//    (16 row pieces of 128 k), the partial of each piece on the diagonal of one MFMA, workgroups
+//    persistent over row groups (or one round of ceil(N / CUs) rows per CU for small layers),
+//    with the neighbouring decode operators fused into its activation load and its output.
+//  * w4_gemv_m8_kernel (M = 2..8, G = 128, K % 256 == 0 up to 20480): the same stream as
+//    8 rows x 128 B per wave instruction, activation fragments held in registers.
+//  * w4_gemv_lds_kernel / w4_gemv_xlds_kernel (the M = 2..8 shapes the previous kernel does
+//    not take): weights or activations staged in LDS.
+//  * w4_gemv_mfma_kernel (the remaining M = 2..8 shapes): 16-row tiles per wave, split K inside
+//    the workgroup, loads issued in batches.
+// The launchers (gemv_plan, launch_gemv and the fused decode entries, end of file) pick the
+// kernel and its layout per shape from the device's CU count.
 //
 // Generic path (any K % 32 == 0, G % 32 == 0, K % G == 0): one wavefront per output row,
 // VALU fp32 FMAs with the exact fp32 dequant, cross-lane reduction.
@@ -36,6 +37,14 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
+// Row-tiled kernel: a wavefront owns RT 16-row tiles of W and a contiguous range of 128-k
+// chunks; the NW wavefronts of a workgroup split K and are reduced through LDS at the end.
+// Lane l = 16 h + r loads 16 bytes of row r (words 4h..4h+3 of the chunk) per chunk, so the
+// wave reads 1 KiB of packed weights per chunk per tile; MFMA A = weights (row i = output
+// feature), B = X^T (column j = batch row, padded to 16). Loads of W and X are issued in
+// batches of UB chunks (up to UB x RT KiB in flight per wave). The workgroup's scales are
+// staged once in LDS, transposed to [group][row], so a lane reads its four rows' scales with
+// one 8-byte LDS read.
 template <int RT, int NW, int UB>
 __global__ __launch_bounds__(NW * kWave) void w4_gemv_mfma_kernel(
     const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
@@ -405,9 +414,19 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
 //    dealt to the NW waves round-robin. A group's pieces are contiguous in Wq, so its blocks
 //    start at any 64-byte piece boundary, and when GR C is not a multiple of 16 the lanes of
 //    the last block past the group's end write to the dummy slot (their loads read the next
-//    group's pieces, or zeros past the buffer). Each diagonal lane writes scale * D[j][j] to an LDS partial
-//    table (double-buffered by group parity); after the group's barrier, 16 lanes per row sum
-//    the row's C partials and wave (i % NW) writes Y.
+//    group's pieces, or zeros past the buffer). Each diagonal lane writes scale * D[j][j] to an
+//    LDS partial table (double-buffered by group parity); after the group's barrier the rows'
+//    C partials are summed either by one wave per row, lane-wise then a wave sum (the "wide"
+//    form: 16-wave plans, groups taller than 16 rows and the one-round layout), or by wave
+//    (i % NW) for all rows, 16 lanes per row; the form fixes the addition order, so entry
+//    points that must give the same bits use the same form.
+// Template parameters: NW waves per workgroup; R ring slots; GR rows per group (0: one round,
+// fz.rows rows per workgroup); XM the activation source (kXPlain: X; kXNorm / kXNormAdd:
+// RMSNorm of the residual, with the add; kXAttn: the merge of the attention splits); YM the
+// output (kYPlain, or kYSwiglu: silu(gate) * up of interleaved row pairs); XV 16-byte
+// activation vectors per thread staged ahead of the weights; FC each lane's activation
+// fragments held in registers for the whole kernel (16 NW a multiple of C); XF the
+// activation loads of every wave issued before any weight load (one barrier between them).
 //  * Blocks stream through a ring of R register slots (R - 1 blocks in flight per wave),
 //    continuing across row groups; the ring's refill cursor (group, slot) advances
 //    incrementally in scalar registers.
@@ -1431,20 +1450,6 @@ hipError_t launch_lds(const GemvArgs& a, hipStream_t st, int grid_cap) {
   return hipSuccess;
 }
 
-// (NW, R) for the M = 1 kernel, from sweeps on MI355X: a 2-slot ring; 16 waves per group
-// when K is long (many blocks per group), 14 when there are many groups (exactly two blocks
-// per wave at K = 3584), otherwise 8.
-void m1_choose(int N, int K, int& nw, int& r) {
-  const int C = K >> 7, groups = (N + 15) / 16;
-  r = 2;
-  if (C >= 64)
-    nw = 16;
-  else if (groups >= 1024 && C >= 14)
-    nw = 14;
-  else
-    nw = 8;
-}
-
 // Launch layout of the M = 1 kernel. The plain and the fused entry points take the same layout
 // for a shape, so they sum its partials in the same order and give the same bits.
 struct M1Layout {
@@ -1508,13 +1513,7 @@ GemvPlan gemv_plan(int M, int N, int K, int G) {
   // LDS-activation kernel when X fits and the weight bytes fit a 31-bit buffer offset.
   const bool small_buf = (size_t)N * (K / 2) + (size_t)16 * K < ((size_t)1 << 31);
   p.m1 = M == 1 && G == 128 && small_buf && m1_bytes(K, 16) <= 96 * 1024;
-  if (p.m1) {
-    m1_choose(N, K, p.nw, p.rt);
-    // 8-row groups when 16-row groups would give each CU only one or two (measured on qkv)
-    const int groups16 = (N + 15) / 16;
-    p.gr = p.nw == 8 && groups16 > 256 && groups16 < 512 && (K / 128) % 2 == 0 ? 8 : 16;
-    return p;
-  }
+  if (p.m1) return p;  // waves, group height and grid come from m1_layout at launch
   // M = 2..8, K a multiple of 256 up to 20480: the half-pair streaming kernel, each wave
   // holding up to five pairs of activation fragments in registers.
   const int P = K / 256;
@@ -1654,7 +1653,7 @@ hipError_t launch_gemv_attn(const GemvArgs& a, const GemvPlan& p, const M1Fuse& 
                             hipStream_t st, int* reject) {
   *reject = 0;
   const int C = a.K >> 7, CP = (C + 15) & ~15;
-  if (!p.m1 || p.rt != 2) {
+  if (!p.m1) {
     *reject = 1;
     return hipSuccess;
   }
@@ -1699,7 +1698,7 @@ hipError_t launch_gemv_fused(const GemvArgs& a, const GemvPlan& p, const M1Fuse&
                              bool swiglu, hipStream_t st, int* reject) {
   *reject = 0;
   const int C = a.K >> 7, CP = (C + 15) & ~15;
-  if (!p.m1 || p.rt != 2 || (swiglu && a.N % 16)) {
+  if (!p.m1 || (swiglu && a.N % 16)) {
     *reject = 1;
     return hipSuccess;
   }

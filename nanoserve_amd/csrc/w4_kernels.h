@@ -20,14 +20,13 @@ struct GemvArgs {
 
 struct GemvPlan {
   bool fast;  // MFMA kernels (K % 128 == 0, G % 128 == 0); otherwise the generic kernel
-  bool m1;    // M = 1 streaming kernel (w4_gemv_m1_kernel); rt holds its ring depth
+  bool m1;    // M = 1 streaming kernel (w4_gemv_m1_kernel)
   bool xlds;  // activations staged in LDS (w4_gemv_xlds_kernel); otherwise in registers
   bool lds;   // weights staged in LDS per 16-row group (w4_gemv_lds_kernel, M = 2..8)
   bool m8;    // M = 2..8 half-pair streaming kernel (w4_gemv_m8_kernel); rt holds its pairs per wave
   int rt;     // 16-row tiles per wavefront
   int nw;     // wavefronts per workgroup splitting K
   int sl;     // scale slab loads per lane per tile (LDS-activation kernel)
-  int gr;     // rows per group of the M = 1 kernel (8 or 16)
 };
 
 bool gemv_fast_path_ok(int M, int N, int K, int G);
