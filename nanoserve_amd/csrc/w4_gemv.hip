@@ -1399,10 +1399,12 @@ hipError_t launch_m8(const GemvArgs& a, int nw, int cap, hipStream_t st) {
 
 // Tile-group height and workgroups per CU for the M = 2..8 kernel with one or two pairs per
 // wave, from a per-CU byte count: every workgroup reads the whole activation (M K bf16, from
-// L2) once and its groups' weights, and the busiest CU sets the time. Ties go to the taller
-// group (fewer group barriers), then to fewer workgroups per CU. On MI355X at M = 8 this picks
-// 32-row groups for qkv (4608 x 3584) and gate/up (37888 x 3584, one workgroup per CU) and
-// 16-row groups for o (3584 x 3584), each the fastest of the candidates measured.
+// L2) once and its groups' weights, and the busiest CU sets the time. Among the plans within 2 %
+// of the cheapest, the one that keeps the most CUs busy wins (more of the chip streams weights),
+// then the taller group (fewer group barriers), then fewer workgroups per CU. On MI355X at
+// M = 8 this picks 16-row groups at one workgroup per CU for qkv (4608 x 3584: 256 workgroups
+// against 144 with 32-row groups, 6.89 -> 6.63 us) and o (3584 x 3584), and 32-row groups for
+// gate/up (37888 x 3584, one workgroup per CU), each the fastest of the candidates measured.
 template <int CW>
 hipError_t launch_m8_auto(const GemvArgs& a, int nw, hipStream_t st) {
   int cus = 0;
@@ -1414,21 +1416,29 @@ hipError_t launch_m8_auto(const GemvArgs& a, int nw, hipStream_t st) {
   if (e != hipSuccess) return e;
   const double xb = 2.0 * a.M * a.K, rowb = 0.5 * a.K;
   const int ntiles = (a.N + 7) / 8;
+  struct Cand {
+    int gt, cap, wgs;
+    double cost;
+  } cand[4];
+  int nc = 0;
   double best = 0;
-  int bgt = 2, bcap = 1;
   for (int gt = 4; gt >= 2; gt -= 2) {
     for (int cap = 1; cap <= min(2, gt == 4 ? pc4 : pc2); ++cap) {
       const int groups = (ntiles + gt - 1) / gt;
       const int wgs = min(groups, cap * cus);
       const int gpw = (groups + wgs - 1) / wgs, wpc = (wgs + cus - 1) / cus;
       const double cost = wpc * (xb + gpw * gt * 8 * rowb);
-      if (best == 0 || cost < 0.98 * best) {
-        best = cost;
-        bgt = gt;
-        bcap = cap;
-      }
+      cand[nc++] = Cand{gt, cap, wgs, cost};
+      if (best == 0 || cost < best) best = cost;
     }
   }
+  int bgt = 2, bcap = 1, bwgs = 0;
+  for (int i = 0; i < nc; ++i)  // candidates come tallest first, then fewer per CU
+    if (cand[i].cost <= 1.02 * best && cand[i].wgs > bwgs) {
+      bgt = cand[i].gt;
+      bcap = cand[i].cap;
+      bwgs = cand[i].wgs;
+    }
   if (bgt == 4) return launch_m8<CW, 4, 4>(a, nw, bcap, st);
   return launch_m8<CW, 2, 2>(a, nw, bcap, st);
 }
