@@ -379,10 +379,11 @@ __device__ __forceinline__ void wait_vmcnt_c() {
 // accumulators through its own part of the LDS ring (step t loads and computes block t KS + ks
 // in every group); at the end groups 1 .. KS-1 hand their accumulators to group 0 through LDS,
 // one group per round, and group 0 adds them in group order and stores the tile.
-// 256-row tiles carry 128 accumulators per lane: the launch bound asks for two workgroups per CU
-// (two waves per SIMD) so the compiler keeps them in VGPRs beside the operands.
+// 256-row tiles carry 128 accumulators per lane: the launch bound asks for two waves per SIMD
+// (two four-wave workgroups per CU, or one eight-wave workgroup with KS = 2) so the compiler
+// keeps them in VGPRs beside the operands.
 template <int BM, int WN, int NWN, int ST, bool SW = false, int KS = 1, int WD = 1>
-__global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 ? 2 : 1) void w4_gemm2_kernel(
+__global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 && KS == 1 ? 2 : 1) void w4_gemm2_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ Wq,
     const uint16_t* __restrict__ S, uint16_t* __restrict__ C, int M, int N, int K, int lgG) {
   constexpr int MI = BM / 32, NJ = WN / 32, BN = WN * NWN;
@@ -621,6 +622,7 @@ constexpr TileCfg kCfgs[] = {
     {128, 128, 1.00f},  // 4: v2, BM 128, 4 waves x 32 cols, 3 stages
     {64, 128, 1.00f},   // 5: v2, BM 64, 4 waves x 32 cols, K split over 2 wave groups, 4 stages
     {256, 128, 1.00f},  // 6: v2, BM 256, 4 waves x 32 cols, 2 stages, two workgroups per CU
+    {256, 128, 1.00f},  // 7: v2, BM 256, K split over 2 wave groups of 4, 2 stages, one per CU
 };
 
 }  // namespace
@@ -644,10 +646,16 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
     // 118 us against 140 for 64 x 128 without the split and 121-125 for a four-way split).
     // 256 x 128 tiles (each wave 256 x 32: one dequantized weight word feeds eight MFMAs, not
     // four) when there are at least four rounds of them on the chip: on MI355X gate/up at
-    // M = 2048 590 -> 555 us; with fewer tiles (gate/up M = 512, down) 128 x 128 is faster.
+    // M = 2048 590 -> 555 us; with fewer tiles (gate/up M = 512) 128 x 128 is faster. When the
+    // 256 x 128 tiles fill between three quarters of the CUs and all of them once and K is long,
+    // one workgroup per CU of eight waves splitting K over two groups (two waves per SIMD on a
+    // single tile, the K loop halved): down 3584 x 18944 at M = 2048 320 -> 301 us and
+    // 303.6 -> 289.7 us on two boxes, 4096 x 14336 263 -> 244 us; 3584 x 3584 (short K) 68 -> 72
+    // and 128 such tiles (half the CUs) 159 -> 206 us, so those keep 128 x 128.
     const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
     const long tiles256 = (long)((M + 255) / 256) * ((N + 127) / 128);
-    const int c = tiles < kCUs ? 5 : tiles256 >= 4 * kCUs ? 6 : 4;
+    const bool ks256 = tiles256 <= kCUs && 4 * tiles256 >= 3 * kCUs && K >= 8192;
+    const int c = tiles < kCUs ? 5 : ks256 ? 7 : tiles256 >= 4 * kCUs ? 6 : 4;
     return GemmPlan{c, kCfgs[c].bm, kCfgs[c].bn};
   }
   int best = 0;
@@ -700,6 +708,10 @@ hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
       hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2, false, 1, kWeightAhead>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
                          a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
+    case 7:
+      hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2, false, 2, kWeightAhead>), grid, dim3(512), 0, st, a.A, a.Wq, a.S,
+                         a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
     default:
       return hipErrorInvalidValue;
   }
@@ -718,6 +730,10 @@ hipError_t launch_gemm_swiglu(const GemmArgs& a, const GemmPlan& p, hipStream_t 
       return hipSuccess;
     case 6:
       hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2, true, 1, kWeightAhead>), grid, dim3(256), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 7:
+      hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2, true, 2, kWeightAhead>), grid, dim3(512), 0, st, a.A, a.Wq,
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     default:

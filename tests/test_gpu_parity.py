@@ -201,17 +201,12 @@ def test_gemm_small(kernels, oracle, M, N, K, G):
     check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G, bf16_weights=True), 2e-5)
 
 
-@pytest.mark.parametrize("name,N,K", [s for s in synth.QWEN7B_LAYERS if s[0] in ("gate_up", "down")],
-                         ids=["gate_up", "down"])
-@pytest.mark.parametrize("M", [512, 2048])
-def test_gemm_configs_sampled_rows(kernels, oracle, name, N, K, M):
-    """Full-size prefill GEMM on the GPU. The float64 oracle checks one row in every 64-row
-    band of M (the smallest M-tile of any GEMM plan, so every output tile of every plan is
-    sampled), every column; every row and column is checked against a plain torch fp32 matmul
-    on the GPU with the same bf16-staged weights, bf16_rne((q - 8) s)."""
-    G = 128
-    print(f"gemm full-size {name} M={M}", flush=True)
-    Wq, S = synth.weights(N, K, G, seed=N + K)
+def _gemm_full_check(kernels, oracle, M, N, K, G, seed):
+    """Prefill GEMM on the GPU. The float64 oracle checks one row in every 64-row band of M (the
+    smallest M-tile of any GEMM plan, so every output tile of every plan is sampled), every
+    column; every row and column is checked against a plain torch fp32 matmul on the GPU with
+    the same bf16-staged weights, bf16_rne((q - 8) s)."""
+    Wq, S = synth.weights(N, K, G, seed=seed)
     X = synth.activations(M, K, seed=7)
     y = run_linear(kernels, X, Wq, S, G)
     band = 64
@@ -227,6 +222,25 @@ def test_gemm_configs_sampled_rows(kernels, oracle, name, N, K, M):
     full = (to_dev(X, torch.bfloat16).float() @ w.t()).cpu().numpy().astype(np.float64)
     del q, w
     check_bf16_faithful(y, full, 3e-5)
+
+
+@pytest.mark.parametrize("name,N,K", [s for s in synth.QWEN7B_LAYERS if s[0] in ("gate_up", "down")],
+                         ids=["gate_up", "down"])
+@pytest.mark.parametrize("M", [512, 2048])
+def test_gemm_configs_sampled_rows(kernels, oracle, name, N, K, M):
+    """Full-size config-4 GEMMs (each M picks a different tile plan: 128 x 128, 256 x 128, the
+    64 x 128 and 256 x 128 K splits inside the workgroup)."""
+    print(f"gemm full-size {name} M={M}", flush=True)
+    _gemm_full_check(kernels, oracle, M, N, K, 128, seed=N + K)
+
+
+@pytest.mark.parametrize("M,N,K", [(1536, 4224, 8192), (2048, 4096, 14336)])
+def test_gemm_ksplit_256_rows(kernels, oracle, M, N, K):
+    """The 256 x 128 plan with K split over two wave groups on the other shapes it takes: 198
+    tiles (6 x 33, fewer than the CUs) at the shortest K it accepts, and 256 tiles (one per
+    CU) of a Llama-3-8B down projection."""
+    print(f"gemm ksplit-256 M={M} N={N} K={K}", flush=True)
+    _gemm_full_check(kernels, oracle, M, N, K, 128, seed=M + N)
 
 
 # ----------------------------------------------------------------- quantizer
