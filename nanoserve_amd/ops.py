@@ -48,6 +48,13 @@ SIGNATURES["ns_probe_empty"] = [_I32, _I32, _VP]
 RESTYPES = {"ns_decode_attention_workspace": _SZ, "ns_w4_gptq_workspace": _SZ}
 
 
+if hasattr(torch._C, "_cuda_getCurrentRawStream"):
+    _raw_stream = torch._C._cuda_getCurrentRawStream
+else:  # pragma: no cover - older torch builds
+    def _raw_stream(device):
+        return torch.cuda.current_stream(device).cuda_stream
+
+
 def _require_gpu_tensor(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
@@ -85,10 +92,11 @@ class Kernels:
             fn.argtypes = args
             fn.restype = RESTYPES.get(name, ctypes.c_int)
 
-    # reference ops.py:32-34: the current torch stream (a hipStream_t on ROCm)
+    # reference ops.py:32-34: the current torch stream (a hipStream_t on ROCm), read as a raw
+    # handle (no Stream object per call: the eager launch path runs this for every operator)
     @staticmethod
     def _stream():
-        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        return ctypes.c_void_p(_raw_stream(torch.cuda.current_device()))
 
     # reference ops.py:36-39
     @staticmethod
@@ -203,7 +211,7 @@ class Kernels:
         rc = self.lib.ns_w4_linear(x.data_ptr(), Wq.data_ptr(), S.data_ptr(), y.data_ptr(), Mp, N,
                                    K, group, self._stream())
         self._check(rc, "ns_w4_linear")
-        return y[:M]
+        return y if Mp == M else y[:M]
 
     # ------------------------------------------------------------------ decoder-step operators
     def rmsnorm(self, x, r, w, eps, out=None):
