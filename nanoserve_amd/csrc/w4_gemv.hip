@@ -1349,11 +1349,12 @@ hipError_t launch_m1_fc(const GemvArgs& a, hipStream_t st, const M1Fuse& fz, int
 }
 
 // FC when 16 NW is a multiple of K / 128; the activation-first barrier (XF) when the layout asks
-// for it, compiled only for the layouts that can hold one workgroup per CU.
+// for it, compiled only for the layouts that take it: one workgroup per CU, and the fused SwiGLU
+// GEMV's two fourteen-wave workgroups per CU.
 template <int NW, int R, int GR, int XM = kXPlain, int YM = kYPlain, int XV = kXVecs>
 hipError_t launch_m1(const GemvArgs& a, hipStream_t st, const M1Fuse& fz = M1Fuse{}, int wpc = 2) {
   const bool fc = (16 * NW) % (a.K >> 7) == 0;
-  if constexpr (GR == 0 || (NW == 16 && GR == 16)) {
+  if constexpr (GR == 0 || (NW == 16 && GR == 16) || (NW == 14 && GR == 16 && YM == kYSwiglu)) {
     if (fz.xfirst) {
       if (fc) return launch_m1_fc<NW, R, GR, XM, YM, XV, true, true>(a, st, fz, wpc);
       return launch_m1_fc<NW, R, GR, XM, YM, XV, false, true>(a, st, fz, wpc);
@@ -1727,7 +1728,11 @@ hipError_t launch_gemv_fused(const GemvArgs& a, const GemvPlan& p, const M1Fuse&
   }
   M1Fuse fz = fz0;
   fz.rows = L.rows;
-  fz.xfirst = L.xfirst;
+  // The fourteen-wave SwiGLU GEMV issues every wave's activation (and norm) loads before any
+  // weight load: decode step 1.370 -> 1.349 ms per token on MI355X (one interleaved run, same
+  // logits); the plain gate/up plan does not gain from it (seven waves, four per CU: 14.47 ->
+  // 14.87 us; fourteen waves with it: 14.08 -> 14.51 us).
+  fz.xfirst = L.xfirst || (swiglu && nw == 14);
   if (L.gr == 0) {
     if (nw == 14) return launch_m1_x<14, 0, kYPlain>(a, fz, norm, st, L.wpc);
     return launch_m1_x<16, 0, kYPlain>(a, fz, norm, st, L.wpc);
