@@ -109,8 +109,10 @@ CONFIG_SHAPES = [synth.QWEN15B_GATE] + list(synth.QWEN7B_LAYERS)
 
 
 @pytest.mark.parametrize("name,N,K", CONFIG_SHAPES, ids=[s[0] for s in CONFIG_SHAPES])
-@pytest.mark.parametrize("M", [1, 8])
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
 def test_gemv_configs(kernels, oracle, name, N, K, M):
+    """Every config shape at M = 1, 2, 4 and 8 (the M = 2..8 planner picks its group height and
+    workgroups per CU per shape and M)."""
     G = 128
     Wq, S = synth.weights(N, K, G, seed=N + K)
     X = synth.activations(M, K, seed=100, per_row_seed=True)
