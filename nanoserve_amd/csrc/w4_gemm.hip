@@ -623,6 +623,8 @@ constexpr TileCfg kCfgs[] = {
     {64, 128, 1.00f},   // 5: v2, BM 64, 4 waves x 32 cols, K split over 2 wave groups, 4 stages
     {256, 128, 1.00f},  // 6: v2, BM 256, 4 waves x 32 cols, 2 stages, two workgroups per CU
     {256, 128, 1.00f},  // 7: v2, BM 256, K split over 2 wave groups of 4, 2 stages, one per CU
+    {128, 64, 1.00f},   // 8: v2, BM 128, K split over 4 wave groups of 2, 2 stages, one per CU
+    {64, 64, 1.00f},    // 9: v2, BM 64, K split over 4 wave groups of 2, 2 stages, two per CU
 };
 
 }  // namespace
@@ -641,9 +643,15 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
   (void)G;
   constexpr int kCUs = 256;
   if (gemm_v2_ok(M, N, K, G)) {
-    // 128 x 128 tiles (three workgroups per CU) unless they leave CUs idle; then 64 x 128 tiles
-    // with K split over two wave groups (eight waves per workgroup; on MI355X down at M = 512:
-    // 118 us against 140 for 64 x 128 without the split and 121-125 for a four-way split).
+    // 128 x 128 tiles (three workgroups per CU) unless they leave CUs idle; then narrower tiles
+    // with K split inside the workgroup over wave groups of two (each wave still a 32-column
+    // slice, four groups): 128 x 64 tiles (one eight-wave workgroup per CU) when those fill
+    // between three quarters of the CUs and all of them, else 64 x 64 tiles (two per CU) when
+    // they fill at most 2.25 rounds of slots, else 64 x 128 tiles split over two groups of four.
+    // On MI355X (one run): down 3584 x 18944 at M = 512 121.8 us (64 x 128, two groups) ->
+    // 102.2 (128 x 64) against 113.0 (64 x 64); 4096 x 14336 at M = 512 98.8 -> 86.2; at M = 256
+    // down 113.6 -> 65.2 and 3584 x 3584 24.7 -> 17.8 (64 x 64, against 94.4 and 24.2 for
+    // 128 x 64); qkv 4608 x 3584 at M = 512 40.0 -> 38.5 (64 x 64; 128 x 64 at 288 tiles: 47.0).
     // 256 x 128 tiles (each wave 256 x 32: one dequantized weight word feeds eight MFMAs, not
     // four) when there are at least four rounds of them on the chip: on MI355X gate/up at
     // M = 2048 590 -> 555 us; with fewer tiles (gate/up M = 512) 128 x 128 is faster. When the
@@ -655,7 +663,12 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
     const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
     const long tiles256 = (long)((M + 255) / 256) * ((N + 127) / 128);
     const bool ks256 = tiles256 <= kCUs && 4 * tiles256 >= 3 * kCUs && K >= 8192;
-    const int c = tiles < kCUs ? 5 : ks256 ? 7 : tiles256 >= 4 * kCUs ? 6 : 4;
+    int c = ks256 ? 7 : tiles256 >= 4 * kCUs ? 6 : 4;
+    if (tiles < kCUs) {
+      const long t128x64 = (long)((M + 127) / 128) * ((N + 63) / 64);
+      const long t64x64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+      c = 4 * t128x64 >= 3 * kCUs && t128x64 <= kCUs ? 8 : 4 * t64x64 <= 9 * kCUs ? 9 : 5;
+    }
     return GemmPlan{c, kCfgs[c].bm, kCfgs[c].bn};
   }
   int best = 0;
@@ -712,6 +725,14 @@ hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
       hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2, false, 2, kWeightAhead>), grid, dim3(512), 0, st, a.A, a.Wq, a.S,
                          a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
+    case 8:
+      hipLaunchKernelGGL((w4_gemm2_kernel<128, 32, 2, 2, false, 4, kWeightAhead>), grid, dim3(512), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 9:
+      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 2, 2, false, 4, kWeightAhead>), grid, dim3(512), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
     default:
       return hipErrorInvalidValue;
   }
@@ -734,6 +755,14 @@ hipError_t launch_gemm_swiglu(const GemmArgs& a, const GemmPlan& p, hipStream_t 
       return hipSuccess;
     case 7:
       hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2, true, 2, kWeightAhead>), grid, dim3(512), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 8:
+      hipLaunchKernelGGL((w4_gemm2_kernel<128, 32, 2, 2, true, 4, kWeightAhead>), grid, dim3(512), 0, st, a.A, a.Wq,
+                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      return hipSuccess;
+    case 9:
+      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 2, 2, true, 4, kWeightAhead>), grid, dim3(512), 0, st, a.A, a.Wq,
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     default:
