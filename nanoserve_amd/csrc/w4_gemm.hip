@@ -639,35 +639,35 @@ bool gemm_v2_ok(int M, int N, int K, int G) {
 }
 
 GemmPlan gemm_plan(int M, int N, int K, int G) {
-  (void)K;
-  (void)G;
-  constexpr int kCUs = 256;
+  int cus = 256;  // the device's CU count (a failed query leaves MI355X's; the launch reports it)
+  if (cached_cu_count(&cus) != hipSuccess || cus <= 0) cus = 256;
   if (gemm_v2_ok(M, N, K, G)) {
-    // 128 x 128 tiles (three workgroups per CU) unless they leave CUs idle; then narrower tiles
-    // with K split inside the workgroup over wave groups of two (each wave still a 32-column
-    // slice, four groups): 128 x 64 tiles (one eight-wave workgroup per CU) when those fill
-    // between three quarters of the CUs and all of them, else 64 x 64 tiles (two per CU) when
-    // they fill at most 2.25 rounds of slots, else 64 x 128 tiles split over two groups of four.
-    // On MI355X (one run): down 3584 x 18944 at M = 512 121.8 us (64 x 128, two groups) ->
-    // 102.2 (128 x 64) against 113.0 (64 x 64); 4096 x 14336 at M = 512 98.8 -> 86.2; at M = 256
-    // down 113.6 -> 65.2 and 3584 x 3584 24.7 -> 17.8 (64 x 64, against 94.4 and 24.2 for
-    // 128 x 64); qkv 4608 x 3584 at M = 512 40.0 -> 38.5 (64 x 64; 128 x 64 at 288 tiles: 47.0).
-    // 256 x 128 tiles (each wave 256 x 32: one dequantized weight word feeds eight MFMAs, not
-    // four) when there are at least four rounds of them on the chip: on MI355X gate/up at
-    // M = 2048 590 -> 555 us; with fewer tiles (gate/up M = 512) 128 x 128 is faster. When the
-    // 256 x 128 tiles fill between three quarters of the CUs and all of them once and K is long,
-    // one workgroup per CU of eight waves splitting K over two groups (two waves per SIMD on a
-    // single tile, the K loop halved): down 3584 x 18944 at M = 2048 320 -> 301 us and
-    // 303.6 -> 289.7 us on two boxes, 4096 x 14336 263 -> 244 us; 3584 x 3584 (short K) 68 -> 72
-    // and 128 such tiles (half the CUs) 159 -> 206 us, so those keep 128 x 128.
+    // Tile plans, measured on MI355X (A/B runs of the four config-4 shapes and the other shapes
+    // quoted):
+    //  * 128 x 128 tiles, three workgroups per CU: the default.
+    //  * 256 x 128 tiles (each wave 256 x 32: one dequantized weight word feeds eight MFMAs, not
+    //    four), two workgroups per CU, when there are at least four rounds of them: gate/up at
+    //    M = 2048 590 -> 555 us; with fewer rounds (gate/up M = 512) 128 x 128 is faster.
+    //  * 256 x 128 tiles with K split over two groups of four waves, one eight-wave workgroup per
+    //    CU (two waves per SIMD on one tile, the K loop halved), when those tiles fill three
+    //    quarters to all of the CUs once and K >= 8192: down 3584 x 18944 at M = 2048 320 -> 301
+    //    and 303.6 -> 289.7 us on two boxes, 4096 x 14336 263 -> 244 us; with short K (3584 x
+    //    3584: 68 -> 72) or 128 such tiles (half the CUs: 159 -> 206) 128 x 128 stays.
+    //  * When 128 x 128 tiles leave CUs idle, narrower tiles with K split four ways over wave
+    //    groups of two (each wave a 32-column slice): 128 x 64 tiles, one eight-wave workgroup per
+    //    CU, when they fill three quarters to all of the CUs (down at M = 512: 121.8 -> 102.2 us,
+    //    4096 x 14336 at M = 512 98.8 -> 86.2); else 64 x 64 tiles, two per CU, up to 2.25 rounds
+    //    (down at M = 256 113.6 -> 65.2 us, 3584 x 3584 24.7 -> 17.8, qkv at M = 512 40.0 -> 38.5;
+    //    128 x 64 tiles there: 94.4, 24.2 and, at 288 tiles, 47.0); else 64 x 128 tiles with K
+    //    split over two groups of four (the plan all of these replaced).
     const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
     const long tiles256 = (long)((M + 255) / 256) * ((N + 127) / 128);
-    const bool ks256 = tiles256 <= kCUs && 4 * tiles256 >= 3 * kCUs && K >= 8192;
-    int c = ks256 ? 7 : tiles256 >= 4 * kCUs ? 6 : 4;
-    if (tiles < kCUs) {
+    const bool ks256 = tiles256 <= cus && 4 * tiles256 >= 3 * cus && K >= 8192;
+    int c = ks256 ? 7 : tiles256 >= 4 * cus ? 6 : 4;
+    if (tiles < cus) {
       const long t128x64 = (long)((M + 127) / 128) * ((N + 63) / 64);
       const long t64x64 = (long)((M + 63) / 64) * ((N + 63) / 64);
-      c = 4 * t128x64 >= 3 * kCUs && t128x64 <= kCUs ? 8 : 4 * t64x64 <= 9 * kCUs ? 9 : 5;
+      c = 4 * t128x64 >= 3 * cus && t128x64 <= cus ? 8 : 4 * t64x64 <= 9 * cus ? 9 : 5;
     }
     return GemmPlan{c, kCfgs[c].bm, kCfgs[c].bn};
   }
@@ -675,7 +675,7 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
   double best_cost = 1e300;
   for (int c = 0; c < 4; ++c) {
     const long tiles = (long)((M + kCfgs[c].bm - 1) / kCfgs[c].bm) * ((N + kCfgs[c].bn - 1) / kCfgs[c].bn);
-    const long rounds = (tiles + kCUs - 1) / kCUs;
+    const long rounds = (tiles + cus - 1) / cus;
     const double cost = (double)rounds * kCfgs[c].bm * kCfgs[c].bn / kCfgs[c].eff;
     if (cost < best_cost) {
       best_cost = cost;
