@@ -125,7 +125,7 @@ def test_decode_qkv(k, pos, with_bias):
 # ------------------------------------------------------------------ ns_decode_attention
 @pytest.mark.parametrize("Hq,Hk", [(28, 4), (7, 1), (4, 4), (8, 1), (16, 4)])
 @pytest.mark.parametrize("max_len,n", [(64, 1), (64, 64), (1024, 63), (1024, 65), (1024, 1024),
-                                       (1100, 1000), (1100, 1100)])
+                                       (1100, 1000), (1100, 1100), (4096, 4000), (16384, 16384)])
 def test_decode_attention(k, Hq, Hk, max_len, n):
     print(f"decode_attention Hq={Hq} Hk={Hk} max_len={max_len} n={n}", flush=True)
     D = 128
@@ -254,7 +254,7 @@ def _attn_chunk(k):
     return next(n for n in range(1, 4097) if ws(28, 4, 128, n + 1) > ws(28, 4, 128, n))
 
 
-@pytest.mark.parametrize("max_len", [200, 600, 2000])
+@pytest.mark.parametrize("max_len", [200, 600, 2000, 4096, 16384])
 def test_gemv_decode_attn_merges_splits(k, max_len):
     """The o GEMV fed by unmerged attention splits equals the merged attention output times
     the same weights (one split: the attention's own bf16 output; several: merged in the
