@@ -605,92 +605,75 @@ __global__ void __launch_bounds__(kAttnBlock)
   }
 }
 
-// Second launch: one workgroup per kv head merges the splits of its R query heads. Split
-// (max, sum) pairs go to LDS first, then every output element's split values are loaded in
-// batches of 16 splits, each batch issued before any is used.
-__global__ void __launch_bounds__(kBlock)
+// Second launch: the splits' partial results merged into the attention output. One workgroup
+// per (query head, 64 dimensions), eight waves, lane = dimension: wave w merges splits w,
+// w + 8, ... with a running maximum (loads issued 16 splits at a time), then wave 0 combines the
+// eight waves' results, each rescaled from its own maximum to the overall one. The grid grows with
+// the query heads, not the splits, so a long context (hundreds of splits) is merged by 56
+// workgroups of short loops (the earlier form, one workgroup per kv head walking every split,
+// took as long as the attention itself at 16384 cache rows).
+constexpr int kMergeWaves = 8;
+__global__ void __launch_bounds__(kMergeWaves * kWave)
     decode_attn_merge_kernel(const float* __restrict__ opart, const float* __restrict__ ml,
                              const int* __restrict__ pos_p, uint16_t* __restrict__ out, int Hq,
-                             int Hk, int max_len) {
+                             int max_len) {
   constexpr int D = kHeadDim;
-  constexpr int SB = 16;             // splits per load batch
-  constexpr int SMAX = 64;           // splits per LDS pass
-  __shared__ float wt[SMAX][kMaxGroup];
-  __shared__ float lsum[SMAX][kMaxGroup];
-  __shared__ float scale_old[kMaxGroup], inv_l[kMaxGroup];
+  constexpr int SB = 16;  // splits per load batch of a wave
+  __shared__ float red_m[kMergeWaves], red_l[kMergeWaves];
+  __shared__ float red_o[kMergeWaves][kWave];
   const int n = min(*pos_p + 1, max_len);
   const int nsplit = n > 0 ? (n + kChunk - 1) / kChunk : 0;
   if (nsplit <= 1) return;  // written by the attention kernel itself
-  const int g = blockIdx.x, R = Hq / Hk, tid = threadIdx.x;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // outputs i = tid + 256k, k < 4 (R * D <= 1024)
-  float m_run = -INFINITY, l_run = 0.f;  // thread tid < R: head tid
-  for (int s0 = 0; s0 < nsplit; s0 += SMAX) {
-    const int ns = min(SMAX, nsplit - s0);
-    float2 st[2];
+  const int h = blockIdx.x, lane = threadIdx.x & (kWave - 1);
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int d = kWave * blockIdx.y + lane;
+  float m_w = -INFINITY, l_w = 0.f, acc = 0.f;
+  // every split below nsplit holds at least one cache row, so its maximum is finite and the
+  // batch maximum below is too (split sb is always in the batch)
+  for (int sb = w; sb < nsplit; sb += kMergeWaves * SB) {
+    float mv[SB], lv[SB], ov[SB];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int i = tid + kBlock * k, sp = i / kMaxGroup, hh = i % kMaxGroup;
-      st[k] = sp < ns && hh < R
-                  ? *reinterpret_cast<const float2*>(&ml[((size_t)(s0 + sp) * Hq + g * R + hh) * 2])
-                  : make_float2(-INFINITY, 0.f);
+    for (int u = 0; u < SB; ++u) {
+      const int sp = sb + kMergeWaves * u;
+      const bool valid = sp < nsplit;
+      const size_t row = (size_t)(valid ? sp : sb) * Hq + h;
+      const float2 m2 = *reinterpret_cast<const float2*>(&ml[row * 2]);
+      mv[u] = valid ? m2.x : -INFINITY;
+      lv[u] = valid ? m2.y : 0.f;
+      ov[u] = valid ? opart[row * D + d] : 0.f;
     }
-    __syncthreads();  // the previous pass is done with wt
+    float mb = m_w;
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int i = tid + kBlock * k;
-      wt[i / kMaxGroup][i % kMaxGroup] = st[k].x;
-      lsum[i / kMaxGroup][i % kMaxGroup] = st[k].y;
+    for (int u = 0; u < SB; ++u) mb = fmaxf(mb, mv[u]);
+    const float f_old = exp2f(m_w - mb);  // 0 for the first batch (m_w = -inf, mb finite)
+    acc *= f_old;
+    l_w *= f_old;
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const float f = exp2f(mv[u] - mb);  // 0 for splits past nsplit
+      acc = fmaf(f, ov[u], acc);
+      l_w = fmaf(f, lv[u], l_w);
     }
-    __syncthreads();
-    if (tid < R) {
-      float mm = m_run;
-      for (int sp = 0; sp < ns; ++sp) mm = fmaxf(mm, wt[sp][tid]);
-      const float f_old = exp2f(m_run - mm);
-      float ll = l_run * f_old;
-      for (int sp = 0; sp < ns; ++sp) {
-        const float f = exp2f(wt[sp][tid] - mm);
-        ll = fmaf(f, lsum[sp][tid], ll);
-        wt[sp][tid] = f;
-      }
-      scale_old[tid] = f_old;
-      m_run = mm;
-      l_run = ll;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = tid + kBlock * k;
-      if (i < R * D) acc[k] *= scale_old[i / D];
-    }
-    for (int sb = 0; sb < ns; sb += SB) {
-      float v[4][SB];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = tid + kBlock * k;
-        const int hh = i / D, d = i % D;
-        const float* src = &opart[((size_t)(s0 + sb) * Hq + g * R + hh) * D + d];
-#pragma unroll
-        for (int u = 0; u < SB; ++u)
-          v[k][u] = i < R * D && sb + u < ns ? src[(size_t)u * Hq * D] : 0.f;
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int i = tid + kBlock * k;
-        const int hh = min(i / D, kMaxGroup - 1);
-#pragma unroll
-        for (int u = 0; u < SB; ++u)
-          if (sb + u < ns) acc[k] = fmaf(wt[sb + u][hh], v[k][u], acc[k]);
-      }
-    }
+    m_w = mb;
   }
-  if (tid < R) inv_l[tid] = 1.f / l_run;
+  if (lane == 0) {
+    red_m[w] = m_w;
+    red_l[w] = l_w;
+  }
+  red_o[w][lane] = acc;
   __syncthreads();
+  if (w != 0) return;
+  float mt = red_m[0];  // finite: wave 0 holds split 0
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int i = tid + kBlock * k;
-    if (i < R * D)
-      out[(size_t)g * R * D + i] = static_cast<uint16_t>(f32_to_bf16_rne(acc[k] * inv_l[i / D]));
+  for (int k = 1; k < kMergeWaves; ++k) mt = fmaxf(mt, red_m[k]);
+  float num = 0.f, den = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMergeWaves; ++k) {
+    const float f = exp2f(red_m[k] - mt);  // 0 for a wave without splits
+    num = fmaf(f, red_o[k][lane], num);
+    den = fmaf(f, red_l[k], den);
   }
+  out[(size_t)h * D + d] = static_cast<uint16_t>(f32_to_bf16_rne(num / den));
 }
 
 // ------------------------------------------------------------------ decode-step start
@@ -766,8 +749,8 @@ int launch_attn(const void* q, const void* bias, const void* inv_freq, void* kc,
   if (merge && splits > 1) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return static_cast<int>(e);
-    hipLaunchKernelGGL(decode_attn_merge_kernel, dim3(Hk), dim3(kBlock), 0, st, opart, ml, pos,
-                       static_cast<uint16_t*>(out), Hq, Hk, max_len);
+    hipLaunchKernelGGL(decode_attn_merge_kernel, dim3(Hq, kHeadDim / kWave), dim3(kMergeWaves * kWave),
+                       0, st, opart, ml, pos, static_cast<uint16_t*>(out), Hq, max_len);
   }
   return last_status();
 }

@@ -38,6 +38,10 @@ import torch.nn.functional as F
 from . import gptq
 from .ops import Kernels
 
+# Cache rows per split of the library's decode attention (its workspace grows by one split
+# every ATTN_SPLIT_ROWS rows; tests/test_abi.py checks the two agree).
+ATTN_SPLIT_ROWS = 128
+
 
 @dataclass(frozen=True)
 class Qwen2Shape:
@@ -263,6 +267,12 @@ class Qwen2Runner:
         self.max_len = max_len
         self.work = self.k.decode_attention_workspace(s.heads, s.kv_heads, s.head_dim, max_len,
                                                       device=self.dev)
+        # Up to 16 cache splits the o projection merges the attention's splits in its own
+        # activation load; past that every o workgroup would read every split's partials, and
+        # the attention's merge kernel followed by the plain o GEMV is faster (MI355X, 28-layer
+        # 7B step at its last position: 1.384 against 1.411 ms at 1024 rows, 1.416 against
+        # 1.410 at 2048, 1.552 against 1.416 at 4096, 2.399 against 1.693 at 16384).
+        self.merge_in_o = max_len <= 16 * ATTN_SPLIT_ROWS
         self.graph = None
 
     def _store_kv(self, li, k, v, pos0):
@@ -281,7 +291,8 @@ class Qwen2Runner:
         Per layer five kernels: the q/k/v GEMV with the residual add + input RMSNorm fused
         into its activation load, the attention (bias + RoPE + KV append + attention over
         128-row splits of the cache), the o GEMV, which merges the attention's splits as it
-        loads its activation, the gate/up GEMV with the post-attention add + RMSNorm fused in
+        loads its activation (for caches of more than 16 splits the attention's own merge
+        kernel merges them and the o GEMV is the plain one), the gate/up GEMV with the post-attention add + RMSNorm fused in
         and SwiGLU fused into its output, and the down GEMV. The residual stream alternates between two
         buffers (a fused GEMV reads one and one of its workgroups writes the other)."""
         s, k = self.shape, self.k
@@ -298,9 +309,13 @@ class Qwen2Runner:
                 resid, spare = spare, resid
             k.decode_qkv_attention(self.qkv[0], L["bqkv"], self.inv_freq, self.pos,
                                    self.cache_k[li], self.cache_v[li], s.heads, s.kv_heads, D,
-                                   self.work, out=self.attn, merge=False, rot=self.rot)
-            k.gemv_decode_attn(self.attn, self.work, self.pos, self.max_len, s.heads, *L["wo"],
-                               G, out=self.o)
+                                   self.work, out=self.attn, merge=not self.merge_in_o,
+                                   rot=self.rot)
+            if self.merge_in_o:
+                k.gemv_decode_attn(self.attn, self.work, self.pos, self.max_len, s.heads,
+                                   *L["wo"], G, out=self.o)
+            else:
+                k.gemv_decode(*L["wo"], G, x=self.attn, out=self.o)
             k.gemv_decode(*L["wgu"], G, res=resid, r=self.o, norm_w=L["ln_post"], eps=eps,
                           res_out=spare, swiglu=True, out=self.act)
             resid, spare = spare, resid

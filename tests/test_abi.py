@@ -180,6 +180,16 @@ def test_decode_attention_workspace_and_rejects(k):
     assert fused(rot=P + 4) == -2               # the rotation table is read 16 bytes at a time
 
 
+def test_runner_split_rows_match_library(k):
+    """The runner's rows per attention split (it picks where the o GEMV stops merging the
+    splits by it) are the library's: the workspace grows by one split every that many rows."""
+    from nanoserve_amd.qwen import ATTN_SPLIT_ROWS
+
+    ws = k.lib.ns_decode_attention_workspace
+    assert ws(28, 4, 128, 1) == ws(28, 4, 128, ATTN_SPLIT_ROWS)
+    assert ws(28, 4, 128, ATTN_SPLIT_ROWS + 1) == 2 * ws(28, 4, 128, ATTN_SPLIT_ROWS)
+
+
 def test_decode_embed_rejects(k):
     """ns_decode_embed checks its sizes and pointers before any HIP call."""
     def call(vocab=1000, H=3584, D=128, tok=P, pos=P, embed=P, x=P, rot=P):

@@ -558,12 +558,15 @@ def test_runner_gptq_calibration(k):
     assert g_c < 0.6 * r_c and g_h < 0.9 * r_h
 
 
-@pytest.mark.parametrize("H,nh,nkv,I,V,T", [(896, 7, 1, 1024, 1000, 12),
-                                             (256, 2, 1, 512, 512, 5),
-                                             (512, 4, 2, 768, 640, 130)])
-def test_runner_matches_hf_qwen2(k, H, nh, nkv, I, V, T):
-    """Prompt pass (GEMV for T <= 8, GEMM above) and four decode steps, eager and graph."""
-    print(f"runner H={H} heads={nh}/{nkv} I={I} V={V} T={T}", flush=True)
+@pytest.mark.parametrize("H,nh,nkv,I,V,T,cache", [(896, 7, 1, 1024, 1000, 12, 0),
+                                                   (256, 2, 1, 512, 512, 5, 0),
+                                                   (512, 4, 2, 768, 640, 130, 0),
+                                                   (512, 4, 2, 768, 640, 130, 2304)])
+def test_runner_matches_hf_qwen2(k, H, nh, nkv, I, V, T, cache):
+    """Prompt pass (GEMV for T <= 8, GEMM above) and four decode steps, eager and graph; with a
+    cache longer than 16 attention splits the steps merge the splits in the attention's own
+    merge kernel and run the plain o GEMV."""
+    print(f"runner H={H} heads={nh}/{nkv} I={I} V={V} T={T} cache={cache}", flush=True)
     m = _hf_model(H, nh, nkv, I, V, layers=2, seed=0)
     runner = Qwen2Runner.from_hf(m, device=DEV, kernels=k)
     ref_model = _effective_hf(m, runner)
@@ -571,7 +574,8 @@ def test_runner_matches_hf_qwen2(k, H, nh, nkv, I, V, T):
     ids = torch.randint(0, V, (T + n_dec,), generator=torch.Generator().manual_seed(1))
     with torch.no_grad():
         ref = ref_model(ids[None]).logits[0]
-    runner.alloc_cache(T + n_dec)
+    runner.alloc_cache(max(T + n_dec, cache))
+    assert runner.merge_in_o == (cache == 0)
     prompt = runner.forward(ids[:T].to(DEV), 0, use_cache=True)
     torch.cuda.synchronize()
     _check_logits(prompt, ref[:T])
