@@ -1,7 +1,8 @@
 // Launch-time device facts, looked up once and then read from tables: the current device's CU
-// count and each kernel's occupancy (workgroups per CU at a block size and dynamic LDS size).
+// count, each kernel's occupancy (workgroups per CU at a block size and dynamic LDS size) and
+// its opt-in to more than 64 KiB of dynamic LDS.
 // A decode step launches hundreds of kernels, so the launch path must not query HIP for these
-// every time; both are keyed by the current device (hipGetDevice), so a process that drives
+// every time; all three are keyed by the current device (hipGetDevice), so a process that drives
 // several GPUs gets each device's own figures.
 #include <atomic>
 #include <mutex>
@@ -26,6 +27,14 @@ struct OccEntry {
 };
 std::mutex g_occ_mu;
 std::vector<OccEntry> g_occ;  // a few dozen entries: one per (kernel, block, LDS size, device)
+
+struct LdsEntry {
+  const void* fn;
+  int dev;
+  hipError_t result;
+};
+std::mutex g_lds_mu;
+std::vector<LdsEntry> g_lds;  // one per (kernel, device) that asked for more than 64 KiB
 
 }  // namespace
 
@@ -66,6 +75,18 @@ hipError_t cached_occupancy(const void* fn, int threads, size_t lds, int* per_cu
   g_occ.push_back(OccEntry{fn, threads, lds, dev, v});
   *per_cu = v;
   return hipSuccess;
+}
+
+hipError_t cached_max_dynamic_lds(const void* fn, int bytes) {
+  int dev = 0;
+  hipError_t e = current_device(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_lds_mu);
+  for (const LdsEntry& l : g_lds)
+    if (l.fn == fn && l.dev == dev) return l.result;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  g_lds.push_back(LdsEntry{fn, dev, e});
+  return e;
 }
 
 }  // namespace ns

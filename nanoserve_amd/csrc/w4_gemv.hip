@@ -1305,9 +1305,8 @@ int xlds_sl(int K, int G, int rt, int nw, int r) {
 template <int RT, int NW, int R, int SL>
 hipError_t launch_xlds(const GemvArgs& a, hipStream_t st) {
   const void* fn = reinterpret_cast<const void*>(&w4_gemv_xlds_kernel<RT, NW, R, SL>);
-  // Opt in once per instantiation to LDS beyond 64 KiB (gfx950 has 160 KiB per CU).
-  static const hipError_t attr =
-      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  // Opt in (once per instantiation and device) to LDS beyond 64 KiB (gfx950 has 160 KiB per CU).
+  const hipError_t attr = cached_max_dynamic_lds(fn, 160 * 1024);
   if (attr != hipSuccess) return attr;
   const size_t lds = xlds_bytes(a.M, a.K, a.G, RT, NW, R, SL);
   int per_cu = 0;
@@ -1327,8 +1326,7 @@ template <int NW, int R, int GR, int XM, int YM, int XV, bool FC, bool XF>
 hipError_t launch_m1_fc(const GemvArgs& a, hipStream_t st, const M1Fuse& fz, int wpc) {
   const void* fn = reinterpret_cast<const void*>(&w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV, FC, XF>);
   // the planner keeps the dynamic part under 96 KiB; the limit leaves room for static LDS
-  static const hipError_t attr =
-      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+  const hipError_t attr = cached_max_dynamic_lds(fn, 128 * 1024);
   if (attr != hipSuccess) return attr;
   const int rows = GR > 0 ? GR : fz.rows;
   if (rows <= 0) return hipErrorInvalidValue;
@@ -1368,8 +1366,7 @@ hipError_t launch_m1(const GemvArgs& a, hipStream_t st, const M1Fuse& fz = M1Fus
 template <int CW, int GT, int R>
 int m8_per_cu(int nw, hipError_t* err) {
   const void* fn = reinterpret_cast<const void*>(&w4_gemv_m8_kernel<CW, GT, R>);
-  static const hipError_t attr =
-      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  const hipError_t attr = cached_max_dynamic_lds(fn, 160 * 1024);
   *err = attr;
   if (attr != hipSuccess) return 0;
   const size_t lds = m8_bytes(nw, CW, GT);
@@ -1447,8 +1444,7 @@ hipError_t launch_m8_auto(const GemvArgs& a, int nw, hipStream_t st) {
 template <int MP, int NW, int CW, int ST, int DPW>
 hipError_t launch_lds(const GemvArgs& a, hipStream_t st, int grid_cap) {
   const void* fn = reinterpret_cast<const void*>(&w4_gemv_lds_kernel<MP, NW, CW, ST, DPW>);
-  static const hipError_t attr =
-      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  const hipError_t attr = cached_max_dynamic_lds(fn, 160 * 1024);
   if (attr != hipSuccess) return attr;
   const size_t lds = lds_bytes(a.K, NW, ST);
   int cus = 0;

@@ -9,6 +9,8 @@ namespace ns {
 // and a kernel's occupancy (workgroups per CU) at a block size and dynamic LDS size.
 hipError_t cached_cu_count(int* cus);
 hipError_t cached_occupancy(const void* fn, int threads, size_t lds, int* per_cu);
+// Opts kernel fn into `bytes` of dynamic LDS on the current device, once per (kernel, device).
+hipError_t cached_max_dynamic_lds(const void* fn, int bytes);
 
 struct GemvArgs {
   const uint16_t* X;

@@ -293,8 +293,7 @@ template <int NW, int GW>
 hipError_t launch_packed_lds(const uint16_t* X, const uint32_t* Wp, const uint16_t* Sp,
                              uint16_t* Y, int M, int N, int K, hipStream_t st) {
   const void* fn = reinterpret_cast<const void*>(&w4_gemv_packed_lds_kernel<NW, GW>);
-  static const hipError_t attr =
-      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 128 * 1024);
+  const hipError_t attr = cached_max_dynamic_lds(fn, 128 * 1024);
   if (attr != hipSuccess) return attr;
   int cus = 0;
   hipError_t e = cached_cu_count(&cus);
