@@ -544,6 +544,31 @@ def main():
         ms_eager = (time.perf_counter() - t0) * 1e3 / args.steps
         extra["config2_m1_eager_gbs"] = round(bytes_m1 / (ms_eager * 1e-3) / 1e9, 1)
 
+        # the same steps as back-to-back launches from a C++ host loop (the reference's own
+        # benchmark method, bench/bench_w4a16.cu:42-78): no graph, no Python between launches
+        def loop_calls(xs, n):
+            out = []
+            for i in range(n):
+                for name, N, K in layers:
+                    wq, s = dev_w[name][i % copies]
+                    out.append((xs[name], wq, s, ys1[name]))
+            return out
+        ys1 = {name: torch.empty(1, N, dtype=torch.bfloat16, device=dev) for name, N, K in layers}
+        warm_calls, main_calls = loop_calls(x1, max(args.warmup, 1)), loop_calls(x1, args.steps)
+        loop_ms = []
+        for _ in range(3):
+            kern.linear_loop(warm_calls, G)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            kern.linear_loop(main_calls, G)
+            e1.record()
+            torch.cuda.synchronize()
+            loop_ms.append(e0.elapsed_time(e1) / args.steps)
+        ms_loop = statistics.median(loop_ms)
+        extra["config2_m1_stream_launch"] = {"us_per_step": round(ms_loop * 1e3, 3),
+                                             "gbs": round(bytes_m1 / (ms_loop * 1e-3) / 1e9, 1)}
+
         # config 1: Qwen2.5-1.5B gate, M=1
         name, N, K = synth.QWEN15B_GATE
         Wq, S = synth.weights(N, K, G, seed=1)

@@ -33,6 +33,17 @@ int ns_probe_read(const void* p, size_t bytes, void* sink, int grid, int waves, 
  */
 int ns_probe_empty(int grid, int threads, void* stream);
 
+/*
+ * The reference's benchmark times back-to-back launches on one stream from its C++ host loop
+ * (bench/bench_w4a16.cu:42-78); this is that loop for bench.py: ns_w4_linear(X[i], Wq[i],
+ * S[i], Y[i], M[i], N[i], K[i], G, stream) for i = 0 .. ncalls - 1, in order, with no host
+ * work between the launches. Returns 0, -2 for NULL arrays or ncalls < 1, or the first
+ * non-zero return of ns_w4_linear (the launches before it were issued).
+ */
+int ns_probe_linear_loop(const void* const* X, const void* const* Wq, const void* const* S,
+                         void* const* Y, const int* M, const int* N, const int* K, int G,
+                         int ncalls, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

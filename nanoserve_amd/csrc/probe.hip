@@ -8,6 +8,7 @@
 #include <stdint.h>
 
 #include "../../include/nanoserve_probe.h"
+#include "../../include/nanoserve_w4.h"
 #include "w4_common.h"
 
 namespace ns {
@@ -71,6 +72,17 @@ int ns_probe_empty(int grid, int threads, void* stream) {
   hipLaunchKernelGGL(ns::probe_empty_kernel, dim3(grid), dim3(threads), 0,
                      static_cast<hipStream_t>(stream));
   return static_cast<int>(hipGetLastError());
+}
+
+int ns_probe_linear_loop(const void* const* X, const void* const* Wq, const void* const* S,
+                         void* const* Y, const int* M, const int* N, const int* K, int G, int ncalls,
+                         void* stream) {
+  if (!X || !Wq || !S || !Y || !M || !N || !K || ncalls < 1) return -2;
+  for (int i = 0; i < ncalls; ++i) {
+    const int rc = ns_w4_linear(X[i], Wq[i], S[i], Y[i], M[i], N[i], K[i], G, stream);
+    if (rc != 0) return rc;
+  }
+  return 0;
 }
 
 }  // extern "C"

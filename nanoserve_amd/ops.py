@@ -45,6 +45,7 @@ SIGNATURES["ns_w4_gptq"] = [_VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_decode_attention_noalloc"] = [_VP, _VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_probe_read"] = [_VP, _SZ, _VP, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_probe_empty"] = [_I32, _I32, _VP]
+SIGNATURES["ns_probe_linear_loop"] = [_VP] * 7 + [_I32, _I32, _VP]
 RESTYPES = {"ns_decode_attention_workspace": _SZ, "ns_w4_gptq_workspace": _SZ}
 
 
@@ -494,3 +495,17 @@ class Kernels:
     def probe_empty(self, grid=1, threads=64):
         """Launch an empty kernel (the per-launch floor of a graph of kernels)."""
         self._check(self.lib.ns_probe_empty(grid, threads, self._stream()), "ns_probe_empty")
+
+    def linear_loop(self, calls, group=128):
+        """Issue ns_w4_linear for each (x, Wq, S, y) of ``calls`` back to back from the C++ host
+        loop of ns_probe_linear_loop (no Python between the launches), on the current stream.
+        Every tensor must satisfy ns_w4_linear's own contract without padding (M <= 8 or a
+        multiple of 128, contiguous, y [M, N])."""
+        n = len(calls)
+        ptrs, ints = ctypes.c_void_p * n, ctypes.c_int * n
+        rc = self.lib.ns_probe_linear_loop(
+            ptrs(*[c[0].data_ptr() for c in calls]), ptrs(*[c[1].data_ptr() for c in calls]),
+            ptrs(*[c[2].data_ptr() for c in calls]), ptrs(*[c[3].data_ptr() for c in calls]),
+            ints(*[c[0].shape[0] for c in calls]), ints(*[c[1].shape[0] for c in calls]),
+            ints(*[c[0].shape[1] for c in calls]), group, n, self._stream())
+        self._check(rc, "ns_probe_linear_loop")

@@ -39,7 +39,7 @@ def test_header_declares_the_reference_entry_points():
         "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention",
         "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn", "ns_decode_embed",
         "ns_bf16_gemv", "ns_w4_gptq_workspace", "ns_w4_gptq", "ns_w4_linear_swiglu",
-        "ns_probe_read", "ns_probe_empty", "ns_decode_attention_noalloc"])
+        "ns_probe_read", "ns_probe_empty", "ns_probe_linear_loop", "ns_decode_attention_noalloc"])
 
 
 def test_library_exports_every_declared_symbol():
