@@ -140,10 +140,10 @@ def main():
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            fn(0)  # allocator warm-up outside capture
+            fn(0)  # allocator warm-up outside capture; makes the stream's K-split workspace
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
-        with torch.cuda.graph(g):
+        with torch.cuda.graph(g, stream=s):  # the stream that ran the warm-up
             for i in range(n):
                 fn(i)
         torch.cuda.synchronize()

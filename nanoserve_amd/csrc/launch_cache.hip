@@ -3,7 +3,8 @@
 // its opt-in to more than 64 KiB of dynamic LDS.
 // A decode step launches hundreds of kernels, so the launch path must not query HIP for these
 // every time; all three are keyed by the current device (hipGetDevice), so a process that drives
-// several GPUs gets each device's own figures.
+// several GPUs gets each device's own figures. The same file keeps the K-split GEMV's
+// per-(device, stream) workspace.
 #include <atomic>
 #include <mutex>
 #include <tuple>
@@ -35,6 +36,14 @@ struct LdsEntry {
 };
 std::mutex g_lds_mu;
 std::vector<LdsEntry> g_lds;  // one per (kernel, device) that asked for more than 64 KiB
+
+struct WsEntry {
+  int dev;
+  hipStream_t stream;
+  void* ws;
+};
+std::mutex g_ws_mu;
+std::vector<WsEntry> g_ws;  // one per (device, stream) that ran a K-split GEMV
 
 }  // namespace
 
@@ -87,6 +96,31 @@ hipError_t cached_max_dynamic_lds(const void* fn, int bytes) {
   e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   g_lds.push_back(LdsEntry{fn, dev, e});
   return e;
+}
+
+hipError_t split_workspace(hipStream_t st, void** ws) {
+  int dev = 0;
+  hipError_t e = current_device(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  for (const WsEntry& w : g_ws)
+    if (w.dev == dev && w.stream == st) {
+      *ws = w.ws;
+      return hipSuccess;
+    }
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(st, &cap);
+  if (e != hipSuccess) return e;
+  if (cap != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
+  void* p = nullptr;
+  e = hipMalloc(&p, kSplitBytes);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // the caller runs unsplit; leave no error for its next check
+    return e;
+  }
+  g_ws.push_back(WsEntry{dev, st, p});
+  *ws = p;
+  return hipSuccess;
 }
 
 }  // namespace ns

@@ -14,7 +14,8 @@
 //    persistent over row groups (or one round of ceil(N / CUs) rows per CU for small layers),
 //    with the neighbouring decode operators fused into its activation load and its output.
 //  * w4_gemv_m8_kernel (M = 2..8, G = 128, K % 256 == 0 up to 20480): the same stream as
-//    8 rows x 128 B per wave instruction, activation fragments held in registers.
+//    8 rows x 128 B per wave instruction, activation fragments held in registers; K of 49
+//    pairs and more run in three K slices whose fp32 partials w4_gemv_m8_merge_kernel sums.
 //  * w4_gemv_lds_kernel / w4_gemv_xlds_kernel (the M = 2..8 shapes the previous kernel does
 //    not take): weights or activations staged in LDS.
 //  * w4_gemv_mfma_kernel (the remaining M = 2..8 shapes): 16-row tiles per wave, split K inside
@@ -1050,7 +1051,8 @@ __device__ __forceinline__ void xpose_rows(u32x4_t (&r)[4]) {
 template <int CW, int GT, int R>
 __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
     const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
-    const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int M, int N, int K) {
+    const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int M, int N, int K, int ks,
+    float* __restrict__ part) {
   constexpr uint32_t kOOB = 0x7fffffc0u;
   constexpr int NB = CW * GT;  // 1 KiB blocks per wave per group
   static_assert(NB % R == 0, "each ring slot serves fixed blocks of a group");
@@ -1069,7 +1071,10 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
   const int c16 = lane & 15, kq = lane >> 4;
   const int ntiles = (N + 7) >> 3;
   const int ngroups = (ntiles + GT - 1) / GT;
-  const int gstep = gridDim.x;
+  // K slices: workgroup b serves slice b % ks (pairs [pa, pb)) of groups b / ks, b / ks + gstep..
+  const int slice = (int)blockIdx.x % ks, ph = (P + ks - 1) / ks;
+  const int pa = slice * ph, pb = min(P, pa + ph);
+  const int gstep = (int)gridDim.x / ks;
   const uint32_t RB = (uint32_t)(K >> 1);  // bytes per weight row
 
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
@@ -1090,8 +1095,8 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
   u32x4_t xa[CW][4];
 #pragma unroll
   for (int t = 0; t < CW; ++t) {
-    const int p = wv + NW * t;
-    const uint32_t so = p < P ? 512u * (uint32_t)p : kOOB;
+    const int p = pa + wv + NW * t;
+    const uint32_t so = p < pb ? 512u * (uint32_t)p : kOOB;
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       xa[t][s] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xres, vx + 64u * s, so, 0));
@@ -1103,8 +1108,8 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
   const uint32_t vs = ((uint32_t)nl * (uint32_t)C + hc) * 2u;
   auto issue = [&](u32x4_t& w, uint32_t& sc, int g, int i) {
     const int t = i / GT, u = i % GT;
-    const int p = wv + NW * t;
-    const bool live = g < ngroups && p < P;
+    const int p = pa + wv + NW * t;
+    const bool live = g < ngroups && p < pb;
     const uint32_t row0 = 8u * (uint32_t)(GT * g + u);
     w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                         wres, vw, live ? row0 * RB + 128u * p : kOOB, kStreamAux));
@@ -1113,7 +1118,7 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
   };
   u32x4_t ring[R];
   uint32_t rsc[R];
-  int g = blockIdx.x;
+  int g = (int)blockIdx.x / ks;
   // With up to three pairs per wave, every wave issues its activation loads before any wave of
   // the workgroup issues weight loads (the CU returns loads in issue order, so a later wave's
   // activation would otherwise wait behind the earlier waves' weight blocks): on MI355X at M = 8
@@ -1214,7 +1219,12 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
         v += pw[q0] + pw[q1];
       }
       const int n = 8 * (GT * g + u) + on;
-      if (om < M && n < N) Y[(size_t)om * N + n] = (uint16_t)f32_to_bf16_rne(v);
+      if (om < M && n < N) {
+        if (ks == 1)
+          Y[(size_t)om * N + n] = (uint16_t)f32_to_bf16_rne(v);
+        else
+          part[((size_t)slice * M + om) * N + n] = v;
+      }
     }
   };
   int it = 0;
@@ -1238,6 +1248,20 @@ __global__ __launch_bounds__(1024) void w4_gemv_m8_kernel(
     }
   }
   for (; g < ngroups; ++it, g += gstep) group(std::false_type{}, it);
+}
+
+// Sums the ks K-slice partials ([ks][M][N] fp32) of the M = 2..8 kernel in slice order and
+// rounds to bf16: a separate launch, so the slices' partials are visible without device-scope
+// fences inside the streaming kernel (on gfx950 such a fence writes back and invalidates the
+// XCD's L2; one per group made the down projection ten times slower).
+__global__ __launch_bounds__(256) void w4_gemv_m8_merge_kernel(const float* __restrict__ part,
+                                                               uint16_t* __restrict__ Y, int MN,
+                                                               int ks) {
+  const int i = (int)(blockIdx.x * 256 + threadIdx.x);
+  if (i >= MN) return;
+  float v = 0.f;
+  for (int s = 0; s < ks; ++s) v += part[(size_t)s * MN + i];
+  Y[i] = (uint16_t)f32_to_bf16_rne(v);
 }
 
 size_t m8_bytes(int nw, int cw, int gt) {
@@ -1379,8 +1403,15 @@ int m8_per_cu(int nw, hipError_t* err) {
   return max(per_cu, 1);
 }
 
+// K slices of the M = 2..8 kernel: ks workgroups share each group, each writing its fp32
+// partials to the stream's split workspace ([ks][M][N]); a merge launch sums them into Y.
+struct M8Split {
+  int ks = 1;
+  float* part = nullptr;
+};
+
 template <int CW, int GT, int R>
-hipError_t launch_m8(const GemvArgs& a, int nw, int cap, hipStream_t st) {
+hipError_t launch_m8(const GemvArgs& a, int nw, int cap, const M8Split& sp, hipStream_t st) {
   hipError_t e;
   const int per_cu = m8_per_cu<CW, GT, R>(nw, &e);
   if (e != hipSuccess) return e;
@@ -1389,9 +1420,15 @@ hipError_t launch_m8(const GemvArgs& a, int nw, int cap, hipStream_t st) {
   e = cached_cu_count(&cus);
   if (e != hipSuccess) return e;
   const int ngroups = ((a.N + 7) / 8 + GT - 1) / GT;
-  const int grid = max(1, min(ngroups, min(max(per_cu, 1), cap) * cus));
-  hipLaunchKernelGGL((w4_gemv_m8_kernel<CW, GT, R>), dim3(grid), dim3(nw * kWave), lds, st, a.X,
-                     a.Wq, a.S, a.Y, a.M, a.N, a.K);
+  // workgroups per slice: every slice serves every group, so the grid is a multiple of ks
+  const int per_slice = max(1, min(ngroups, min(max(per_cu, 1), cap) * cus / sp.ks));
+  hipLaunchKernelGGL((w4_gemv_m8_kernel<CW, GT, R>), dim3(per_slice * sp.ks), dim3(nw * kWave), lds,
+                     st, a.X, a.Wq, a.S, a.Y, a.M, a.N, a.K, sp.ks, sp.part);
+  if (sp.ks > 1) {
+    const int mn = a.M * a.N;
+    hipLaunchKernelGGL(w4_gemv_m8_merge_kernel, dim3((mn + 255) / 256), dim3(256), 0, st, sp.part,
+                       a.Y, mn, sp.ks);
+  }
   return hipSuccess;
 }
 
@@ -1404,7 +1441,7 @@ hipError_t launch_m8(const GemvArgs& a, int nw, int cap, hipStream_t st) {
 // against 144 with 32-row groups, 6.89 -> 6.63 us) and o (3584 x 3584), and 32-row groups for
 // gate/up (37888 x 3584, one workgroup per CU), each the fastest of the candidates measured.
 template <int CW>
-hipError_t launch_m8_auto(const GemvArgs& a, int nw, hipStream_t st) {
+hipError_t launch_m8_auto(const GemvArgs& a, int nw, const M8Split& sp, hipStream_t st) {
   int cus = 0;
   hipError_t e = cached_cu_count(&cus);
   if (e != hipSuccess) return e;
@@ -1412,7 +1449,7 @@ hipError_t launch_m8_auto(const GemvArgs& a, int nw, hipStream_t st) {
   if (e != hipSuccess) return e;
   const int pc4 = m8_per_cu<CW, 4, 4>(nw, &e);
   if (e != hipSuccess) return e;
-  const double xb = 2.0 * a.M * a.K, rowb = 0.5 * a.K;
+  const double xb = 2.0 * a.M * a.K / sp.ks, rowb = 0.5 * a.K / sp.ks;
   const int ntiles = (a.N + 7) / 8;
   struct Cand {
     int gt, cap, wgs;
@@ -1423,8 +1460,8 @@ hipError_t launch_m8_auto(const GemvArgs& a, int nw, hipStream_t st) {
   for (int gt = 4; gt >= 2; gt -= 2) {
     for (int cap = 1; cap <= min(2, gt == 4 ? pc4 : pc2); ++cap) {
       const int groups = (ntiles + gt - 1) / gt;
-      const int wgs = min(groups, cap * cus);
-      const int gpw = (groups + wgs - 1) / wgs, wpc = (wgs + cus - 1) / cus;
+      const int wgs = max(1, min(groups, cap * cus / sp.ks));
+      const int gpw = (groups + wgs - 1) / wgs, wpc = (sp.ks * wgs + cus - 1) / cus;
       const double cost = wpc * (xb + gpw * gt * 8 * rowb);
       cand[nc++] = Cand{gt, cap, wgs, cost};
       if (best == 0 || cost < best) best = cost;
@@ -1437,8 +1474,8 @@ hipError_t launch_m8_auto(const GemvArgs& a, int nw, hipStream_t st) {
       bcap = cand[i].cap;
       bwgs = cand[i].wgs;
     }
-  if (bgt == 4) return launch_m8<CW, 4, 4>(a, nw, bcap, st);
-  return launch_m8<CW, 2, 2>(a, nw, bcap, st);
+  if (bgt == 4) return launch_m8<CW, 4, 4>(a, nw, bcap, sp, st);
+  return launch_m8<CW, 2, 2>(a, nw, bcap, sp, st);
 }
 
 template <int MP, int NW, int CW, int ST, int DPW>
@@ -1506,6 +1543,14 @@ hipError_t m1_layout(int N, int K, M1Layout* L) {
 
 }  // namespace
 
+// Pairs per wave (cw) and waves (nw) of the M = 2..8 kernel for one of ks K slices: up to 16
+// waves, each holding the fewest pairs that cover the slice (K < 256: one pair, no waves).
+void m8_shape(int K, int ks, int* cw, int* nw) {
+  const int ph = (K / 256 + ks - 1) / ks;
+  *cw = max(1, (ph + 15) / 16);
+  *nw = (ph + *cw - 1) / *cw;
+}
+
 // Register-X kernel limits: scale staging must fit comfortably in LDS next to the reduction.
 bool gemv_fast_path_ok(int M, int N, int K, int G) {
   (void)N;
@@ -1523,13 +1568,18 @@ GemvPlan gemv_plan(int M, int N, int K, int G) {
   if (p.m1) return p;  // waves, group height and grid come from m1_layout at launch
   // M = 2..8, K a multiple of 256 up to 20480: the half-pair streaming kernel, each wave
   // holding up to five pairs of activation fragments in registers.
-  const int P = K / 256;
-  const int cw = (P + 15) / 16;
-  p.m8 = M >= 2 && G == 128 && K % 256 == 0 && cw <= 5 && small_buf &&
+  int cw = 0;
+  m8_shape(K, 1, &cw, &p.nw);
+  p.m8 = M >= 2 && G == 128 && K >= 256 && K % 256 == 0 && cw <= 5 && small_buf &&
          (size_t)M * K * 2 < ((size_t)1 << 31);
   if (p.m8) {
     p.rt = cw;
-    p.nw = (P + cw - 1) / cw;
+    // Four or five pairs per wave leave registers for a two-block ring only, and a workgroup
+    // (one per CU) reads the whole activation for its one or two groups: such K run in three
+    // slices of two pairs per wave, each workgroup streaming three times the rows against a
+    // third of the activation, plus a merge launch. On MI355X at M = 8, down (3584 x 18944):
+    // 18.87 us unsplit, 17.70 in two slices, 16.81 in three, 17.03 in four.
+    p.ks = cw >= 4 ? 3 : 1;
     return p;
   }
   // M = 2..8 with whole rows of a 16-row group in LDS (K <= 4096): weights staged in LDS.
@@ -1587,12 +1637,24 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
     return fc7 ? launch_m1<7, 2, 8>(a, st, fz, L.wpc) : launch_m1<8, 2, 8>(a, st, fz, L.wpc);
   }
   if (p.m8) {
-    switch (p.rt) {
-      case 1: return launch_m8_auto<1>(a, p.nw, st);
-      case 2: return launch_m8_auto<2>(a, p.nw, st);
-      case 3: return launch_m8<3, 2, 2>(a, p.nw, 2, st);
-      case 4: return launch_m8<4, 2, 2>(a, p.nw, 2, st);
-      case 5: return launch_m8<5, 2, 2>(a, p.nw, 2, st);
+    // the K split needs this stream's workspace (made on first use outside graph capture);
+    // without one the kernel runs unsplit
+    M8Split sp;
+    if (p.ks > 1 && (size_t)p.ks * a.M * a.N * 4 <= kSplitBytes) {
+      void* ws = nullptr;
+      if (split_workspace(st, &ws) == hipSuccess) {
+        sp.ks = p.ks;
+        sp.part = static_cast<float*>(ws);
+      }
+    }
+    int cw = 0, nw = 0;
+    m8_shape(a.K, sp.ks, &cw, &nw);
+    switch (cw) {
+      case 1: return launch_m8_auto<1>(a, nw, sp, st);
+      case 2: return launch_m8_auto<2>(a, nw, sp, st);
+      case 3: return launch_m8<3, 2, 2>(a, nw, 2, sp, st);
+      case 4: return launch_m8<4, 2, 2>(a, nw, 2, sp, st);
+      case 5: return launch_m8<5, 2, 2>(a, nw, 2, sp, st);
       default: return hipErrorInvalidValue;
     }
   }

@@ -12,6 +12,14 @@ hipError_t cached_occupancy(const void* fn, int threads, size_t lds, int* per_cu
 // Opts kernel fn into `bytes` of dynamic LDS on the current device, once per (kernel, device).
 hipError_t cached_max_dynamic_lds(const void* fn, int bytes);
 
+// Workspace of the K-split M = 2..8 GEMV (its slices' fp32 partials), kSplitBytes per
+// (device, stream): made on the stream's first request and never freed (graphs captured later
+// hold its address); hipErrorStreamCaptureUnsupported while the stream is being captured and
+// has none yet. Launches that overlap on one stream's workspace (a graph replayed on another
+// stream beside eager work on this one) race.
+constexpr size_t kSplitBytes = (size_t)4 << 20;
+hipError_t split_workspace(hipStream_t st, void** ws);
+
 struct GemvArgs {
   const uint16_t* X;
   const uint32_t* Wq;
@@ -29,6 +37,7 @@ struct GemvPlan {
   int rt;     // 16-row tiles per wavefront
   int nw;     // wavefronts per workgroup splitting K
   int sl;     // scale slab loads per lane per tile (LDS-activation kernel)
+  int ks;     // K slices of the M = 2..8 kernel (1: unsplit)
 };
 
 bool gemv_fast_path_ok(int M, int N, int K, int G);

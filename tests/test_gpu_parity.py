@@ -122,6 +122,60 @@ def test_gemv_configs(kernels, oracle, name, N, K, M):
     check_bf16_faithful(y, ref, 2e-5)
 
 
+@pytest.mark.parametrize("N,K,Ms", [(200, 12544, (2, 5, 8)), (3584, 18944, (3, 6, 7)),
+                                    (1000, 20480, (2, 8)), (4104, 16384, (4, 8))])
+def test_gemv_ksplit(kernels, oracle, N, K, Ms):
+    """M = 2..8 at K with four or five pairs per wave, where the kernel runs in two K slices
+    whose fp32 partials a merge launch sums: every M listed, ragged N (row groups cut by N), and
+    each call repeated bit for bit after calls of other shapes through the same workspace."""
+    G = 128
+    Wq, S = synth.weights(N, K, G, seed=N + 3 * K)
+    wd, sd = to_dev(Wq, torch.int32), to_dev(S, torch.bfloat16)
+    first = {}
+    for M in Ms:
+        X = synth.activations(M, K, seed=M + 40, per_row_seed=True)
+        xd = to_dev(X, torch.bfloat16)
+        y = kernels.w4_linear(xd, wd, sd, G)
+        torch.cuda.synchronize()
+        got = synth.bf16_bits_to_f32(to_host_bits(y)).astype(np.float64)
+        check_bf16_faithful(got, oracle.linear_f64(X, Wq, S, G), 2e-5)
+        first[M] = (xd, to_host_bits(y))
+    for M in reversed(Ms):
+        xd, bits = first[M]
+        np.testing.assert_array_equal(to_host_bits(kernels.w4_linear(xd, wd, sd, G)), bits)
+
+
+def test_gemv_ksplit_graph(kernels, oracle):
+    """The K-split M = 8 GEMV under graph capture: on a stream that already ran it eagerly (its
+    workspace exists) every replay equals the eager result bit for bit, with eager calls between
+    replays; on a fresh stream capture runs the unsplit kernel, still within the oracle's
+    tolerance."""
+    N, K, G, M = 1024, 18944, 128, 8
+    Wq, S = synth.weights(N, K, G, seed=91)
+    X = synth.activations(M, K, seed=92, per_row_seed=True)
+    ref = oracle.linear_f64(X, Wq, S, G)
+    xd, wd, sd = to_dev(X, torch.bfloat16), to_dev(Wq, torch.int32), to_dev(S, torch.bfloat16)
+    for warm in (True, False):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            eager = kernels.w4_linear(xd, wd, sd, G) if warm else None
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            y = kernels.w4_linear(xd, wd, sd, G)
+        for _ in range(3):
+            g.replay()
+            torch.cuda.synchronize()
+            got = synth.bf16_bits_to_f32(to_host_bits(y)).astype(np.float64)
+            check_bf16_faithful(got, ref, 2e-5)
+            if warm:
+                assert torch.equal(y, eager)
+                with torch.cuda.stream(s):
+                    kernels.w4_linear(xd[:3], wd, sd, G)
+                torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_gemv_every_m(kernels, oracle, M):
     N, K, G = 200, 1024, 128       # N not a multiple of 16: row-tile tail
