@@ -51,7 +51,7 @@ int ns_w4_quantize(const void* W, void* Wq, void* S, int N, int K, int G, void* 
  * violates K % 32, G % 32 or K % G returns -2 (the reference calls exit()); a GEMM shape with
  * K % G != 0 returns -2 (the reference reads past the scale row); M, N, K <= 0, NULL
  * pointers, X or Wq not 16-byte aligned, or S or Y not 2-byte aligned return -2.
- * M = 2..8 with K >= 12544 runs in three K slices plus a merge launch, through a 4 MiB
+ * M = 2..8 with K > 8192 runs in two or three K slices plus a merge launch, through a 4 MiB
  * workspace the library makes once per (device, stream), outside graph capture (a captured
  * stream without one runs unsplit); calls overlapping on one stream's workspace race.
  */

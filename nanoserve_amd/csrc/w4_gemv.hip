@@ -14,8 +14,8 @@
 //    persistent over row groups (or one round of ceil(N / CUs) rows per CU for small layers),
 //    with the neighbouring decode operators fused into its activation load and its output.
 //  * w4_gemv_m8_kernel (M = 2..8, G = 128, K % 256 == 0 up to 20480): the same stream as
-//    8 rows x 128 B per wave instruction, activation fragments held in registers; K of 49
-//    pairs and more run in three K slices whose fp32 partials w4_gemv_m8_merge_kernel sums.
+//    8 rows x 128 B per wave instruction, activation fragments held in registers; K of more
+//    than 32 pairs (256 k each) runs in K slices whose fp32 partials w4_gemv_m8_merge_kernel sums.
 //  * w4_gemv_lds_kernel / w4_gemv_xlds_kernel (the M = 2..8 shapes the previous kernel does
 //    not take): weights or activations staged in LDS.
 //  * w4_gemv_mfma_kernel (the remaining M = 2..8 shapes): 16-row tiles per wave, split K inside
@@ -1574,12 +1574,17 @@ GemvPlan gemv_plan(int M, int N, int K, int G) {
          (size_t)M * K * 2 < ((size_t)1 << 31);
   if (p.m8) {
     p.rt = cw;
-    // Four or five pairs per wave leave registers for a two-block ring only, and a workgroup
-    // (one per CU) reads the whole activation for its one or two groups: such K run in three
-    // slices of two pairs per wave, each workgroup streaming three times the rows against a
-    // third of the activation, plus a merge launch. On MI355X at M = 8, down (3584 x 18944):
-    // 18.87 us unsplit, 17.70 in two slices, 16.81 in three, 17.03 in four.
-    p.ks = cw >= 4 ? 3 : 1;
+    // Past 32 pairs (three to five per wave, leaving registers for a two-block ring only, and a
+    // workgroup per CU reading the whole activation for its one or two groups) K runs in the
+    // fewest slices of at most two pairs per wave, each workgroup streaming ks times the rows
+    // against 1 / ks of the activation, plus a merge launch. On MI355X at M = 8 (interleaved
+    // A/B, us): 1536 x 8960 9.1 unsplit -> 7.9 in two slices (8.3 in three); 2048 x 11008
+    // 11.4 -> 8.7 (9.9); 4096 x 14336 14.4 in two, 16.4 in three; 3584 x 18944 18.87 -> 16.81 in
+    // three (17.70 in two); at 32 pairs and fewer every split was slower (3584 x 8192 9.2 ->
+    // 9.5 / 10.3, 7168 x 5120 8.4 -> 10.3). M = 2 and 4 follow (2048 x 11008 at M = 2:
+    // 8.6 -> 7.7).
+    const int P = K / 256;
+    p.ks = P > 32 ? (P + 31) / 32 : 1;
     return p;
   }
   // M = 2..8 with whole rows of a 16-row group in LDS (K <= 4096): weights staged in LDS.

@@ -123,11 +123,13 @@ def test_gemv_configs(kernels, oracle, name, N, K, M):
 
 
 @pytest.mark.parametrize("N,K,Ms", [(200, 12544, (2, 5, 8)), (3584, 18944, (3, 6, 7)),
-                                    (1000, 20480, (2, 8)), (4104, 16384, (4, 8))])
+                                    (1000, 20480, (2, 8)), (4104, 16384, (4, 8)),
+                                    (1536, 8960, (2, 8)), (264, 8448, (3, 8))])
 def test_gemv_ksplit(kernels, oracle, N, K, Ms):
-    """M = 2..8 at K with four or five pairs per wave, where the kernel runs in two K slices
-    whose fp32 partials a merge launch sums: every M listed, ragged N (row groups cut by N), and
-    each call repeated bit for bit after calls of other shapes through the same workspace."""
+    """M = 2..8 at K of more than 32 pairs (256 k each), where the kernel runs in two or three
+    K slices whose fp32 partials a merge launch sums: every M listed, ragged N (row groups cut by
+    N), and each call repeated bit for bit after calls of other shapes through the same
+    workspace."""
     G = 128
     Wq, S = synth.weights(N, K, G, seed=N + 3 * K)
     wd, sd = to_dev(Wq, torch.int32), to_dev(S, torch.bfloat16)
