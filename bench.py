@@ -127,13 +127,16 @@ def main():
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream()
+    # K-split workspaces of the M = 8 layers (ns_w4_linear_ws; the down projection, K = 18944,
+    # runs in three K slices; the other layers need none)
+    ws8 = {name: kern.w4_linear_workspace(8, N, K, G, device=dev) for name, N, K in layers}
 
     def step(xs, i, which=None):
         for name, N, K in layers:
             if which is not None and name != which:
                 continue
             wq, s = dev_w[name][i % copies]
-            kern.w4_linear(xs[name], wq, s, G)
+            kern.w4_linear(xs[name], wq, s, G, work=ws8[name] if xs is x8 else None)
 
     def graph_of(fn, n):
         g = torch.cuda.CUDAGraph()
@@ -161,6 +164,42 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1)  # ms
 
+    def steady_ms(g, n, warm_ms=20.0, rounds=7):
+        """Per-launch ms of a graph of n launches: replays until warm_ms of GPU time have passed
+        (the core clock settles under sustained load: right after an idle gap the same graph
+        ran 3-25 % slower on MI355X), then the median of `rounds` single replays."""
+        spent = 0.0
+        for _ in range(200):
+            spent += time_graph(g)
+            if spent >= warm_ms:
+                break
+        return statistics.median(time_graph(g) for _ in range(rounds)) / n
+
+    wall_khz = kern.wall_clock_khz()
+    clk0 = torch.zeros(32, dtype=torch.int64, device=dev)
+    clk1 = torch.zeros(32, dtype=torch.int64, device=dev)
+
+    def clock_mhz(fn, n):
+        """Average core clock (MHz) over the n launches of fn, replayed warm: ns_probe_clock before
+        and after them in one graph; the median over the XCDs both probes reached."""
+        def body(i):
+            if i == 0:
+                kern.probe_clock(clk0)
+            fn(i)
+            if i == n - 1:
+                kern.probe_clock(clk1)
+        g = graph_of(body, n)
+        steady_ms(g, n, rounds=1)
+        clk0.fill_(-1)
+        clk1.fill_(-1)
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = clk0.view(16, 2).cpu().tolist(), clk1.view(16, 2).cpu().tolist()
+        per_xcd = [(t1 - t0) / (w1 - w0) * wall_khz / 1e3 for (t0, w0), (t1, w1) in zip(a, b)
+                   if min(t0, w0, t1, w1) >= 0 and w1 > w0]
+        del g
+        return round(statistics.median(per_xcd), 1) if per_xcd else None
+
     def deq_f32(wq, s):
         """Plain-torch fp32 dequantization on the GPU (the reference's CPU loop restated,
         bench/bench_w4a16.cu:156-173): nibble i of word j is k = 8j + i, w = (q - 8) * s."""
@@ -186,7 +225,10 @@ def main():
                 cases.append((512, dev_bits(synth.activations(512, K, seed=512), torch.bfloat16)))
             for M, x in cases:
                 y = kern.w4_linear(x, wq, s, G)
-                errs[f"{name}_m{M}"] = max_rel(y, x.float() @ w.t())
+                ref = x.float() @ w.t()
+                errs[f"{name}_m{M}"] = max_rel(y, ref)
+                if M == 8 and ws8[name] is not None:  # the K-split form the M = 8 set times
+                    errs[f"{name}_m8_ksplit"] = max_rel(kern.w4_linear(x, wq, s, G, work=ws8[name]), ref)
             del w
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
@@ -236,8 +278,7 @@ def main():
             for grid, waves, depth in shapes:
                 g = graph_of(lambda i: kern.probe_read(bufs[i % nbuf], grid, waves, depth, sink),
                              2 * nbuf)
-                time_graph(g)
-                us = statistics.median(time_graph(g) for _ in range(3)) / (2 * nbuf) * 1e3
+                us = steady_ms(g, 2 * nbuf, warm_ms=10.0, rounds=3) * 1e3
                 if best is None or us < best[0]:
                     best = (us, grid, waves, depth)
                 del g
@@ -260,8 +301,7 @@ def main():
                 ws = dev_w[name]
                 reps = 6
                 g = graph_of(lambda i: kern.w4_linear(xa, *ws[i % copies], G), reps)
-                time_graph(g)
-                ms = statistics.median(time_graph(g) for _ in range(3)) / reps
+                ms = steady_ms(g, reps)
                 tf = synth.gemm_flops(M, N, K) / (ms * 1e-3) / 1e12
                 gemm[f"{name}_m{M}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
                                         "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
@@ -431,14 +471,12 @@ def main():
 
             for name, N, K in layers:
                 g = graph_of(lambda i, name=name: run(i, which=name), n_launch)
-                time_graph(g)
-                ms = statistics.median(time_graph(g) for _ in range(3)) / n_launch
+                ms = steady_ms(g, n_launch)
                 b = synth.gemv_bytes(M, N, K, G)
                 res[f"{name}_m{M}"] = {"us": round(ms * 1e3, 3), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
                                        "packed": ok[name]}
             g = graph_of(lambda i: run(i), 4 * copies)
-            time_graph(g)
-            ms = statistics.median(time_graph(g) for _ in range(3)) / (4 * copies)
+            ms = steady_ms(g, 4 * copies)
             b = sum(synth.gemv_bytes(M, N, K, G) for _, N, K in layers)
             res[f"set_m{M}"] = {"us": round(ms * 1e3, 3), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
                                 "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -455,8 +493,7 @@ def main():
 
     def m8_set():
         g8 = graph_of(lambda i: step(x8, i), 4 * copies)
-        time_graph(g8)
-        ms8 = statistics.median(time_graph(g8) for _ in range(3)) / (4 * copies)
+        ms8 = steady_ms(g8, 4 * copies)
         bytes_m8 = sum(synth.gemv_bytes(8, N, K, G) for _, N, K in layers)
         return {"gbs": round(bytes_m8 / (ms8 * 1e-3) / 1e9, 1), "us_per_step": round(ms8 * 1e3, 3),
                 "frac_hbm": round(bytes_m8 / (ms8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -467,8 +504,7 @@ def main():
 
     if args.m1_only:
         g1 = graph_of(lambda i: step(x1, i), 4 * copies)
-        time_graph(g1)
-        ms1 = statistics.median(time_graph(g1) for _ in range(3)) / (4 * copies)
+        ms1 = steady_ms(g1, 4 * copies)
         bytes_set = sum(synth.gemv_bytes(1, N, K, G) for _, N, K in layers)
         print(json.dumps({"config2_m1_set": {
             "gbs": round(bytes_set / (ms1 * 1e-3) / 1e9, 1), "us_per_step": round(ms1 * 1e3, 3)},
@@ -493,11 +529,12 @@ def main():
         ms_step = ms_total / args.steps
         value = bytes_m1 / (ms_step * 1e-3) / 1e9
 
-    # ---------------- dominant kernel: gate+up GEMV, M=1, back-to-back launches
+    # ---------------- dominant kernel: gate+up GEMV, M=1, back-to-back launches, timed warm
+    # (steady_ms) with the core clock of the same launches recorded beside it
     n_launch = 4 * copies
     g_gu = graph_of(lambda i: step(x1, i, which="gate_up"), n_launch)
-    time_graph(g_gu)
-    ms_gu = statistics.median(time_graph(g_gu) for _ in range(5)) / n_launch
+    ms_gu = steady_ms(g_gu, n_launch)
+    mhz_gu = clock_mhz(lambda i: step(x1, i, which="gate_up"), n_launch)
     N_gu, K_gu = [(N, K) for n, N, K in layers if n == "gate_up"][0]
     bytes_gu = synth.gemv_bytes(1, N_gu, K_gu, G)
     achieved = bytes_gu / (ms_gu * 1e-3) / 1e9
@@ -505,7 +542,11 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": profiled_traffic(TRAFFIC_PROFILE),
                 "kernel": "w4_gemv_m1_kernel<7, 2, 16, 0, 0, 4, true> (gate_up 37888x3584, M=1)",
-                "bytes_per_launch": bytes_gu, "avg_launch_us": round(ms_gu * 1e3, 3)}
+                "bytes_per_launch": bytes_gu, "avg_launch_us": round(ms_gu * 1e3, 3),
+                "core_clock_mhz": mhz_gu,
+                "timing": "hip events on the launch stream around graph replays of "
+                          f"{n_launch} launches on rotating weight copies, after >= 20 ms of "
+                          "warm replays; median of 7"}
 
     if args.dominant_only:
         print(json.dumps({"roofline": roofline, "launches": 6 * n_launch}), flush=True)
@@ -522,13 +563,14 @@ def main():
         for name, N, K in layers:
             for M, xs in ((1, x1), (8, x8)):
                 g = graph_of(lambda i, name=name, xs=xs: step(xs, i, which=name), n_launch)
-                time_graph(g)
-                ms = statistics.median(time_graph(g) for _ in range(3)) / n_launch
+                ms = steady_ms(g, n_launch)
                 b = synth.gemv_bytes(M, N, K, G)
                 per_layer[f"{name}_m{M}"] = {"us": round(ms * 1e3, 3),
                                              "gbs": round(b / (ms * 1e-3) / 1e9, 1),
                                              "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                              "frac_ceiling": round(ceil["read"][name]["us"] / (ms * 1e3), 4)}
+                if M == 8 and ws8[name] is not None:
+                    per_layer[f"{name}_m{M}"]["entry"] = "ns_w4_linear_ws (K split)"
         extra["per_layer"] = per_layer
 
         extra["config3_m8_set"] = m8_set()
@@ -578,8 +620,7 @@ def main():
         c1w = [(wq0, s0)] + [(wq0.clone(), s0.clone()) for _ in range(c1n - 1)]
         xc1 = dev_bits(synth.activations(1, K, seed=3), torch.bfloat16)
         g1 = graph_of(lambda i: kern.w4_linear(xc1, *c1w[i % c1n], G), 2 * c1n)
-        time_graph(g1)
-        ms1 = statistics.median(time_graph(g1) for _ in range(3)) / (2 * c1n)
+        ms1 = steady_ms(g1, 2 * c1n)
         b1 = synth.gemv_bytes(1, N, K, G)
         extra["config1_gate_m1"] = {"us": round(ms1 * 1e3, 3), "gbs": round(b1 / (ms1 * 1e-3) / 1e9, 1)}
         del c1w, wq0, s0

@@ -51,12 +51,34 @@ int ns_w4_quantize(const void* W, void* Wq, void* S, int N, int K, int G, void* 
  * violates K % 32, G % 32 or K % G returns -2 (the reference calls exit()); a GEMM shape with
  * K % G != 0 returns -2 (the reference reads past the scale row); M, N, K <= 0, NULL
  * pointers, X or Wq not 16-byte aligned, or S or Y not 2-byte aligned return -2.
- * M = 2..8 with K > 8192 runs in two or three K slices plus a merge launch, through a 4 MiB
- * workspace the library makes once per (device, stream), outside graph capture (a captured
- * stream without one runs unsplit); calls overlapping on one stream's workspace race.
+ * Every shape runs as one pass over K: the call allocates nothing, keeps no state and gives
+ * the same bits on every call (eager or inside graph capture). ns_w4_linear_ws below is the
+ * same operation with the decode GEMV's K split.
  */
 int ns_w4_linear(const void* X, const void* Wq, const void* S, void* Y, int M, int N, int K,
                  int G, void* stream);
+
+/*
+ * No counterpart in the reference (its C ABI has only ns_w4_linear, nanoserve_ops.cu:73-90).
+ * Bytes of device workspace ns_w4_linear_ws uses for this shape: ks * M * N * 4 when the
+ * M = 2..8 decode GEMV splits K into ks slices (K > 8192 at G = 128: ks = ceil(K / 8192)),
+ * 0 for every other shape (and for shapes ns_w4_linear rejects).
+ */
+size_t ns_w4_linear_workspace(int M, int N, int K, int G);
+
+/*
+ * No counterpart in the reference. ns_w4_linear with a caller-provided workspace for the K
+ * split of the M = 2..8 decode GEMV (long rows, e.g. the 7B down projection K = 18944): the
+ * slices write fp32 partials [ks][M][N] to `work` and a second launch sums them in slice order
+ * and rounds to bf16. Same arithmetic and tolerance as ns_w4_linear, deterministic, but another
+ * fp32 summation order (outputs may differ from ns_w4_linear's by one bf16 ulp). Shapes whose
+ * ns_w4_linear_workspace is 0 run exactly as ns_w4_linear (work may then be NULL).
+ * Returns -2 when the shape needs a workspace and work is NULL, not 16-byte aligned or smaller
+ * than ns_w4_linear_workspace(M, N, K, G); otherwise as ns_w4_linear. Calls that overlap in
+ * time need workspaces of their own.
+ */
+int ns_w4_linear_ws(const void* X, const void* Wq, const void* S, void* Y, int M, int N, int K,
+                    int G, void* work, size_t work_bytes, void* stream);
 
 /*
  * No counterpart in the reference (its README:149-151 names a Marlin-style pre-shuffled weight

@@ -32,18 +32,9 @@ std::vector<OccEntry> g_occ;  // a few dozen entries: one per (kernel, block, LD
 struct LdsEntry {
   const void* fn;
   int dev;
-  hipError_t result;
 };
 std::mutex g_lds_mu;
 std::vector<LdsEntry> g_lds;  // one per (kernel, device) that asked for more than 64 KiB
-
-struct WsEntry {
-  int dev;
-  hipStream_t stream;
-  void* ws;
-};
-std::mutex g_ws_mu;
-std::vector<WsEntry> g_ws;  // one per (device, stream) that ran a K-split GEMV
 
 }  // namespace
 
@@ -92,35 +83,11 @@ hipError_t cached_max_dynamic_lds(const void* fn, int bytes) {
   if (e != hipSuccess) return e;
   std::lock_guard<std::mutex> lock(g_lds_mu);
   for (const LdsEntry& l : g_lds)
-    if (l.fn == fn && l.dev == dev) return l.result;
+    if (l.fn == fn && l.dev == dev) return hipSuccess;
   e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  g_lds.push_back(LdsEntry{fn, dev, e});
+  // only a success is remembered: after a failure the next launch asks again
+  if (e == hipSuccess) g_lds.push_back(LdsEntry{fn, dev});
   return e;
-}
-
-hipError_t split_workspace(hipStream_t st, void** ws) {
-  int dev = 0;
-  hipError_t e = current_device(&dev);
-  if (e != hipSuccess) return e;
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  for (const WsEntry& w : g_ws)
-    if (w.dev == dev && w.stream == st) {
-      *ws = w.ws;
-      return hipSuccess;
-    }
-  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-  e = hipStreamIsCapturing(st, &cap);
-  if (e != hipSuccess) return e;
-  if (cap != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
-  void* p = nullptr;
-  e = hipMalloc(&p, kSplitBytes);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();  // the caller runs unsplit; leave no error for its next check
-    return e;
-  }
-  g_ws.push_back(WsEntry{dev, st, p});
-  *ws = p;
-  return hipSuccess;
 }
 
 }  // namespace ns

@@ -32,8 +32,14 @@ int ns_w4_quantize(const void* W, void* Wq, void* S, int N, int K, int G, void* 
   return last_status();
 }
 
-int ns_w4_linear(const void* X, const void* Wq, const void* S, void* Y, int M, int N, int K,
-                 int G, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// ns_w4_linear and ns_w4_linear_ws: the same checks and dispatch; `ws` (may be null) is the
+// K-split GEMV's partials buffer.
+int w4_linear(const void* X, const void* Wq, const void* S, void* Y, int M, int N, int K, int G,
+              void* ws, size_t ws_bytes, void* stream) {
   if (M <= 0 || N <= 0 || K <= 0 || G <= 0) return -2;
   if (!X || !Wq || !S || !Y) return -2;
   if (!aligned(X, 16) || !aligned(Wq, 16) || !aligned(S, 2) || !aligned(Y, 2)) return -2;
@@ -47,7 +53,7 @@ int ns_w4_linear(const void* X, const void* Wq, const void* S, void* Y, int M, i
   if (M <= 8) {
     if (!fmt_ok) return -2;
     const ns::GemvArgs a{x, wq, s, y, M, N, K, G};
-    e = ns::launch_gemv(a, ns::gemv_plan(M, N, K, G), st);
+    e = ns::launch_gemv(a, ns::gemv_plan(M, N, K, G), st, static_cast<float*>(ws), ws_bytes);
   } else if (M % 128 == 0 && N % 128 == 0 && fmt_ok) {
     const ns::GemmArgs a{x, wq, s, y, M, N, K, G};
     e = ns::launch_gemm(a, ns::gemm_plan(M, N, K, G), st);
@@ -56,6 +62,26 @@ int ns_w4_linear(const void* X, const void* Wq, const void* S, void* Y, int M, i
   }
   if (e != hipSuccess) return static_cast<int>(e);
   return last_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+int ns_w4_linear(const void* X, const void* Wq, const void* S, void* Y, int M, int N, int K,
+                 int G, void* stream) {
+  return w4_linear(X, Wq, S, Y, M, N, K, G, nullptr, 0, stream);
+}
+
+size_t ns_w4_linear_workspace(int M, int N, int K, int G) {
+  return ns::gemv_split_bytes(M, N, K, G);
+}
+
+int ns_w4_linear_ws(const void* X, const void* Wq, const void* S, void* Y, int M, int N, int K,
+                    int G, void* work, size_t work_bytes, void* stream) {
+  const size_t need = ns::gemv_split_bytes(M, N, K, G);
+  if (need > 0 && (!work || work_bytes < need || !aligned(work, 16))) return -2;
+  return w4_linear(X, Wq, S, Y, M, N, K, G, need > 0 ? work : nullptr, work_bytes, stream);
 }
 
 int ns_w4_linear_swiglu(const void* X, const void* Wq, const void* S, void* Y, int M, int N,

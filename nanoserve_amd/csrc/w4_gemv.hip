@@ -1610,7 +1610,14 @@ GemvPlan gemv_plan(int M, int N, int K, int G) {
   return p;
 }
 
-hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
+size_t gemv_split_bytes(int M, int N, int K, int G) {
+  if (M < 2 || M > 8 || N <= 0 || K <= 0 || G <= 0 || K % 32 || G % 32 || K % G) return 0;
+  const GemvPlan p = gemv_plan(M, N, K, G);
+  return p.fast && p.m8 && p.ks > 1 ? (size_t)p.ks * M * N * sizeof(float) : 0;
+}
+
+hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st, float* ws,
+                       size_t ws_bytes) {
   if (!p.fast) {
     hipLaunchKernelGGL((w4_gemv_generic_kernel<8>), dim3((a.N + 3) / 4), dim3(256), 0, st, a.X,
                        a.Wq, a.S, a.Y, a.M, a.N, a.K, a.G);
@@ -1642,15 +1649,12 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st) {
     return fc7 ? launch_m1<7, 2, 8>(a, st, fz, L.wpc) : launch_m1<8, 2, 8>(a, st, fz, L.wpc);
   }
   if (p.m8) {
-    // the K split needs this stream's workspace (made on first use outside graph capture);
-    // without one the kernel runs unsplit
+    // the K split runs only in the caller's workspace (ns_w4_linear_ws); ns_w4_linear passes
+    // none and runs every shape unsplit
     M8Split sp;
-    if (p.ks > 1 && (size_t)p.ks * a.M * a.N * 4 <= kSplitBytes) {
-      void* ws = nullptr;
-      if (split_workspace(st, &ws) == hipSuccess) {
-        sp.ks = p.ks;
-        sp.part = static_cast<float*>(ws);
-      }
+    if (p.ks > 1 && ws && (size_t)p.ks * a.M * a.N * sizeof(float) <= ws_bytes) {
+      sp.ks = p.ks;
+      sp.part = ws;
     }
     int cw = 0, nw = 0;
     m8_shape(a.K, sp.ks, &cw, &nw);

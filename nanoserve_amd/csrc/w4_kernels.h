@@ -12,13 +12,9 @@ hipError_t cached_occupancy(const void* fn, int threads, size_t lds, int* per_cu
 // Opts kernel fn into `bytes` of dynamic LDS on the current device, once per (kernel, device).
 hipError_t cached_max_dynamic_lds(const void* fn, int bytes);
 
-// Workspace of the K-split M = 2..8 GEMV (its slices' fp32 partials), kSplitBytes per
-// (device, stream): made on the stream's first request and never freed (graphs captured later
-// hold its address); hipErrorStreamCaptureUnsupported while the stream is being captured and
-// has none yet. Launches that overlap on one stream's workspace (a graph replayed on another
-// stream beside eager work on this one) race.
-constexpr size_t kSplitBytes = (size_t)4 << 20;
-hipError_t split_workspace(hipStream_t st, void** ws);
+// K-split M = 2..8 GEMV: the slices' fp32 partials [ks][M][N] live in a caller-provided
+// workspace (ns_w4_linear_ws); without one the kernel runs unsplit.
+size_t gemv_split_bytes(int M, int N, int K, int G);
 
 struct GemvArgs {
   const uint16_t* X;
@@ -42,7 +38,9 @@ struct GemvPlan {
 
 bool gemv_fast_path_ok(int M, int N, int K, int G);
 GemvPlan gemv_plan(int M, int N, int K, int G);
-hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st);
+// ws / ws_bytes: the K-split workspace (gemv_split_bytes); nullptr runs every shape unsplit.
+hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st,
+                       float* ws = nullptr, size_t ws_bytes = 0);
 
 // Neighbouring operators fused into the M = 1 GEMV (w4_gemv_m1_kernel):
 //   XM == kXNorm:    the activation is rmsnorm(res) * nw;

@@ -40,13 +40,18 @@ SIGNATURES["ns_bf16_gemv"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _I32, _I32, _V
 SIGNATURES["ns_w4_repack"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_w4_linear_packed"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_w4_linear_swiglu"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
+SIGNATURES["ns_w4_linear_workspace"] = [_I32, _I32, _I32, _I32]
+SIGNATURES["ns_w4_linear_ws"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _SZ, _VP]
 SIGNATURES["ns_w4_gptq_workspace"] = [_I32]
 SIGNATURES["ns_w4_gptq"] = [_VP, _VP, _VP, _VP, _VP, _SZ, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_decode_attention_noalloc"] = [_VP, _VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_probe_read"] = [_VP, _SZ, _VP, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_probe_empty"] = [_I32, _I32, _VP]
 SIGNATURES["ns_probe_linear_loop"] = [_VP] * 7 + [_I32, _I32, _VP]
-RESTYPES = {"ns_decode_attention_workspace": _SZ, "ns_w4_gptq_workspace": _SZ}
+SIGNATURES["ns_probe_clock"] = [_VP, _VP]
+SIGNATURES["ns_probe_wall_clock_khz"] = [ctypes.POINTER(ctypes.c_int)]
+RESTYPES = {"ns_decode_attention_workspace": _SZ, "ns_w4_gptq_workspace": _SZ,
+            "ns_w4_linear_workspace": _SZ}
 
 
 if hasattr(torch._C, "_cuda_getCurrentRawStream"):
@@ -181,13 +186,22 @@ class Kernels:
         self._check(rc, "ns_w4_gptq")
         return Wq, S
 
-    def w4_linear(self, x, Wq, S, group=128, out=None):
+    def w4_linear_workspace(self, M, N, K, group=128, device=None):
+        """A uint8 device tensor of the workspace ``w4_linear(..., work=)`` uses for this shape
+        (the K split of the M = 2..8 GEMV for K > 8192), or None when the shape needs none."""
+        n = int(self.lib.ns_w4_linear_workspace(M, N, K, group))
+        return torch.empty(n, dtype=torch.uint8, device=device or "cuda") if n else None
+
+    def w4_linear(self, x, Wq, S, group=128, out=None, work=None):
         """x [M, K] bf16 -> y [M, N] bf16 = x @ deq(Wq, S)^T. Reference ops.py:85-97.
 
         M <= 8 runs natively (the reference pads 3 -> 4 and 5..7 -> 8 with zero rows, which
         does not change any output row); larger M is padded with zero rows up to a multiple
         of 128, as the reference does. ``out`` (not in the reference): a contiguous [M, N]
-        bf16 tensor to write instead of a new one, for M that needs no padding."""
+        bf16 tensor to write instead of a new one, for M that needs no padding. ``work`` (not in
+        the reference): a workspace from ``w4_linear_workspace``; with it the M = 2..8 GEMV
+        splits long rows over K (ns_w4_linear_ws), without it every shape runs unsplit
+        (ns_w4_linear)."""
         _require_gpu_tensor(x, "x", torch.bfloat16)
         _require_gpu_tensor(Wq, "Wq", torch.int32)
         _require_gpu_tensor(S, "S", torch.bfloat16)
@@ -209,9 +223,16 @@ class Kernels:
             y = out
         else:
             y = torch.empty((Mp, N), dtype=torch.bfloat16, device=x.device)
-        rc = self.lib.ns_w4_linear(x.data_ptr(), Wq.data_ptr(), S.data_ptr(), y.data_ptr(), Mp, N,
-                                   K, group, self._stream())
-        self._check(rc, "ns_w4_linear")
+        if work is None:
+            rc = self.lib.ns_w4_linear(x.data_ptr(), Wq.data_ptr(), S.data_ptr(), y.data_ptr(), Mp,
+                                       N, K, group, self._stream())
+            self._check(rc, "ns_w4_linear")
+        else:
+            _require_gpu_tensor(work, "work", torch.uint8)
+            rc = self.lib.ns_w4_linear_ws(x.data_ptr(), Wq.data_ptr(), S.data_ptr(), y.data_ptr(),
+                                          Mp, N, K, group, work.data_ptr(), work.numel(),
+                                          self._stream())
+            self._check(rc, "ns_w4_linear_ws")
         return y if Mp == M else y[:M]
 
     # ------------------------------------------------------------------ decoder-step operators
@@ -495,6 +516,21 @@ class Kernels:
     def probe_empty(self, grid=1, threads=64):
         """Launch an empty kernel (the per-launch floor of a graph of kernels)."""
         self._check(self.lib.ns_probe_empty(grid, threads, self._stream()), "ns_probe_empty")
+
+    def probe_clock(self, out):
+        """Store each XCD's (shader-clock cycles, wall-clock ticks) into ``out`` (a contiguous
+        GPU int64 tensor of 32 elements: XCD x in out[2x], out[2x + 1]) from one launch on the
+        current stream (include/nanoserve_probe.h)."""
+        _require_gpu_tensor(out, "out", torch.int64)
+        if out.numel() != 32 or not out.is_contiguous():
+            raise ValueError("out must be a contiguous int64 tensor of 32 elements")
+        self._check(self.lib.ns_probe_clock(out.data_ptr(), self._stream()), "ns_probe_clock")
+
+    def wall_clock_khz(self):
+        """The current device's wall-clock rate in kHz (the tick rate probe_clock records)."""
+        v = ctypes.c_int(0)
+        self._check(self.lib.ns_probe_wall_clock_khz(ctypes.byref(v)), "ns_probe_wall_clock_khz")
+        return v.value
 
     def linear_loop(self, calls, group=128):
         """Issue ns_w4_linear for each (x, Wq, S, y) of ``calls`` back to back from the C++ host

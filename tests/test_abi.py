@@ -39,7 +39,8 @@ def test_header_declares_the_reference_entry_points():
         "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention",
         "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn", "ns_decode_embed",
         "ns_bf16_gemv", "ns_w4_gptq_workspace", "ns_w4_gptq", "ns_w4_linear_swiglu",
-        "ns_probe_read", "ns_probe_empty", "ns_probe_linear_loop", "ns_decode_attention_noalloc"])
+        "ns_probe_read", "ns_probe_empty", "ns_probe_linear_loop", "ns_decode_attention_noalloc",
+        "ns_w4_linear_workspace", "ns_w4_linear_ws", "ns_probe_clock", "ns_probe_wall_clock_khz"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -147,6 +148,35 @@ def test_decode_qkv_rejects_bad_arguments(k):
     assert k.lib.ns_decode_qkv(P, None, P, P, P, P, 28, 4, 128, 0, None) == -2
     assert k.lib.ns_decode_qkv(P, None, P, None, P, P, 28, 4, 128, 64, None) == -2
     assert k.lib.ns_decode_qkv(P, P + 2, P, P, P, P, 28, 4, 128, 64, None) == -2
+
+
+def test_linear_workspace_sizes_and_rejects(k):
+    """The K-split workspace is needed only by the M = 2..8 GEMV past 32 pairs (K > 8192) and is
+    ks * M * N fp32 partials, ks = ceil(K / 8192); ns_w4_linear_ws rejects a missing, short or
+    misaligned workspace before any HIP call."""
+    ws = k.lib.ns_w4_linear_workspace
+    assert ws(8, 3584, 18944, 128) == 3 * 8 * 3584 * 4
+    assert ws(2, 1536, 8960, 128) == 2 * 2 * 1536 * 4
+    assert ws(4, 4104, 16384, 128) == 2 * 4 * 4104 * 4
+    assert ws(8, 3584, 8192, 128) == 0      # 32 pairs: one pass
+    assert ws(1, 3584, 18944, 128) == 0     # M = 1 kernel
+    assert ws(9, 3584, 18944, 128) == 0     # not a GEMV shape
+    assert ws(128, 3584, 18944, 128) == 0   # GEMM
+    assert ws(8, 3584, 18944, 64) == 0      # generic GEMV (G % 128 != 0)
+    assert ws(8, 3584, 18944, 100) == 0     # invalid format
+    assert ws(0, 3584, 18944, 128) == 0
+    P = 1 << 20
+    need = ws(8, 64, 18944, 128)
+    call = k.lib.ns_w4_linear_ws
+    assert call(P, P, P, P, 8, 64, 18944, 128, None, need, None) == -2
+    assert call(P, P, P, P, 8, 64, 18944, 128, P, need - 4, None) == -2
+    assert call(P, P, P, P, 8, 64, 18944, 128, P + 8, need, None) == -2
+    # shapes ns_w4_linear rejects are rejected the same way, workspace or not
+    assert call(P, P, P, P, 9, 64, 18944, 128, P, need, None) == -2
+    assert call(P, P, P, P, 8, 64, 18944, 100, P, need, None) == -2
+    assert k.lib.ns_probe_clock(None, None) == -2
+    assert k.lib.ns_probe_clock(P + 4, None) == -2
+    assert k.lib.ns_probe_wall_clock_khz(None) == -2
 
 
 def test_decode_attention_workspace_and_rejects(k):

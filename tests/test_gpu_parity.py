@@ -71,29 +71,65 @@ def test_reference_case_linear(kernels, oracle, ref_case, M):
 
 
 # ----------------------------------------------------------------- bit-exact dequant probes
-def _onehot_probe(kernels, oracle, N, K, G, M, staged, seed):
+def _onehot_probe(kernels, oracle, N, K, G, M, staged, seed, ks=None, call=None):
     """X rows are unit vectors e_k, so y[m][n] = w[n][k_m] with no rounding but the bf16 output:
-    y must equal bf16_rne of the (exact or bf16-staged) dequantized weight, bit for bit."""
+    y must equal bf16_rne of the (exact or bf16-staged) dequantized weight, bit for bit.
+    ``ks``: the k probed (default every k); ``call(x, Wq, S)``: the entry point (default
+    w4_linear)."""
     Wq, S = synth.weights(N, K, G, seed=seed)
     Wq[0, :] = 0x00000000            # q = 0 -> -8 everywhere in row 0
     Wq[1, :] = 0xFFFFFFFF            # q = 15 -> 7 everywhere in row 1
     deq = oracle.dequant_bf16(Wq, S, G) if staged else oracle.f32_to_bf16(oracle.dequant_f32(Wq, S, G))
     wq_d, s_d = to_dev(Wq, torch.int32), to_dev(S, torch.bfloat16)
-    for k0 in range(0, K, M):
-        ks = [k for k in range(k0, min(k0 + M, K))]
+    call = call or (lambda x, w, sc: kernels.w4_linear(x, w, sc, G))
+    ks = list(range(K)) if ks is None else list(ks)
+    for i0 in range(0, len(ks), M):
+        kk = ks[i0:i0 + M]
         X = np.zeros((M, K), dtype=np.uint16)
-        for m, k in enumerate(ks):
+        for m, k in enumerate(kk):
             X[m, k] = 0x3F80          # 1.0
-        y = kernels.w4_linear(to_dev(X, torch.bfloat16), wq_d, s_d, G)
+        y = call(to_dev(X, torch.bfloat16), wq_d, s_d)
         torch.cuda.synchronize()
-        got = to_host_bits(y)
-        for m, k in enumerate(ks):
+        got = to_host_bits(y).reshape(M, -1)
+        for m, k in enumerate(kk):
             np.testing.assert_array_equal(got[m], deq[:, k], err_msg=f"k={k}")
 
 
 @pytest.mark.parametrize("G", [128, 256])
 def test_gemv_dequant_bitexact(kernels, oracle, G):
     _onehot_probe(kernels, oracle, N=80, K=512, G=G, M=8, staged=False, seed=G)
+
+
+# M = 1 layouts of w4_gemv_m1_kernel (the launcher picks them from N and K on the device's CU
+# count): the one-round layout (N = 80, K = 512), seven-wave persistent 16-row groups with the
+# activation fragments held in registers (gate/up-like, N = 16400, K = 1792), eight-row groups
+# (N = 8000, K = 4096) and sixteen-wave workgroups for long rows (K = 8192). Long rows are
+# probed at every k of their first and last 256 and at a seeded sample in between, which covers
+# every nibble, word, piece and block position.
+M1_PROBES = [(80, 512), (16400, 1792), (8000, 4096), (64, 8192)]
+
+
+def _m1_probe_ks(K, seed):
+    if K <= 2048:
+        return range(K)
+    mid = np.random.default_rng(seed).choice(np.arange(256, K - 256), 256, replace=False)
+    return sorted(set(range(256)) | set(range(K - 256, K)) | set(int(k) for k in mid))
+
+
+@pytest.mark.parametrize("N,K", M1_PROBES)
+def test_gemv_m1_dequant_bitexact(kernels, oracle, N, K):
+    """The M = 1 kernel (ns_w4_linear at M = 1) returns each dequantized weight bit for bit."""
+    _onehot_probe(kernels, oracle, N=N, K=K, G=128, M=1, staged=False, seed=N + K,
+                  ks=_m1_probe_ks(K, N))
+
+
+@pytest.mark.parametrize("N,K", M1_PROBES)
+def test_gemv_decode_dequant_bitexact(kernels, oracle, N, K):
+    """The fused decode GEMV (ns_w4_gemv_decode with a plain activation: no norm, no SwiGLU)
+    returns each dequantized weight bit for bit on the same layouts."""
+    _onehot_probe(kernels, oracle, N=N, K=K, G=128, M=1, staged=False, seed=N + K + 1,
+                  ks=_m1_probe_ks(K, N + 1),
+                  call=lambda x, w, sc: kernels.gemv_decode(w, sc, 128, x=x[0]))
 
 
 def test_gemv_generic_dequant_bitexact(kernels, oracle):
@@ -126,56 +162,82 @@ def test_gemv_configs(kernels, oracle, name, N, K, M):
                                     (1000, 20480, (2, 8)), (4104, 16384, (4, 8)),
                                     (1536, 8960, (2, 8)), (264, 8448, (3, 8))])
 def test_gemv_ksplit(kernels, oracle, N, K, Ms):
-    """M = 2..8 at K of more than 32 pairs (256 k each), where the kernel runs in two or three
-    K slices whose fp32 partials a merge launch sums: every M listed, ragged N (row groups cut by
-    N), and each call repeated bit for bit after calls of other shapes through the same
-    workspace."""
+    """M = 2..8 at K of more than 32 pairs (256 k each): through ns_w4_linear_ws the kernel runs
+    in two or three K slices whose fp32 partials a merge launch sums, through ns_w4_linear in one
+    pass. Both within half a bf16 ulp (+2e-5 ||ref||) of the oracle, every M listed, ragged N
+    (row groups cut by N), and each call repeated bit for bit after calls of other shapes (the
+    workspace reused; ns_w4_linear keeps nothing between calls)."""
     G = 128
     Wq, S = synth.weights(N, K, G, seed=N + 3 * K)
     wd, sd = to_dev(Wq, torch.int32), to_dev(S, torch.bfloat16)
+    work = kernels.w4_linear_workspace(max(Ms), N, K, G)
+    assert work is not None and work.numel() == -(-K // 8192) * max(Ms) * N * 4
     first = {}
     for M in Ms:
         X = synth.activations(M, K, seed=M + 40, per_row_seed=True)
         xd = to_dev(X, torch.bfloat16)
-        y = kernels.w4_linear(xd, wd, sd, G)
-        torch.cuda.synchronize()
-        got = synth.bf16_bits_to_f32(to_host_bits(y)).astype(np.float64)
-        check_bf16_faithful(got, oracle.linear_f64(X, Wq, S, G), 2e-5)
-        first[M] = (xd, to_host_bits(y))
-    for M in reversed(Ms):
-        xd, bits = first[M]
-        np.testing.assert_array_equal(to_host_bits(kernels.w4_linear(xd, wd, sd, G)), bits)
+        ref = oracle.linear_f64(X, Wq, S, G)
+        for w in (work, None):
+            y = kernels.w4_linear(xd, wd, sd, G, work=w)
+            torch.cuda.synchronize()
+            check_bf16_faithful(synth.bf16_bits_to_f32(to_host_bits(y)).astype(np.float64), ref,
+                                2e-5)
+            first[(M, w is None)] = (xd, to_host_bits(y))
+    for (M, unsplit), (xd, bits) in reversed(list(first.items())):
+        y = kernels.w4_linear(xd, wd, sd, G, work=None if unsplit else work)
+        np.testing.assert_array_equal(to_host_bits(y), bits)
+
+
+def test_gemv_linear_ws_rejects(kernels):
+    """ns_w4_linear_ws needs a workspace of ns_w4_linear_workspace bytes where the shape splits,
+    and takes none where it does not (the call is then ns_w4_linear)."""
+    lib = kernels.lib
+    assert lib.ns_w4_linear_workspace(8, 3584, 18944, 128) == 3 * 8 * 3584 * 4
+    assert lib.ns_w4_linear_workspace(8, 3584, 8192, 128) == 0      # 32 pairs: one pass
+    assert lib.ns_w4_linear_workspace(1, 3584, 18944, 128) == 0     # M = 1
+    assert lib.ns_w4_linear_workspace(128, 3584, 18944, 128) == 0   # GEMM
+    x = torch.zeros(8, 18944, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(64, 18944 // 8, dtype=torch.int32, device="cuda")
+    s = torch.zeros(64, 148, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty(8, 64, dtype=torch.bfloat16, device="cuda")
+    need = lib.ns_w4_linear_workspace(8, 64, 18944, 128)
+    work = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    args = (x.data_ptr(), w.data_ptr(), s.data_ptr(), y.data_ptr(), 8, 64, 18944, 128)
+    assert lib.ns_w4_linear_ws(*args, None, 0, None) == -2
+    assert lib.ns_w4_linear_ws(*args, work.data_ptr(), need - 4, None) == -2
+    assert lib.ns_w4_linear_ws(*args, work.data_ptr() + 4, need - 4, None) == -2
+    assert lib.ns_w4_linear_ws(*args, work.data_ptr(), need, None) == 0
+    small = (x.data_ptr(), w.data_ptr(), s.data_ptr(), y.data_ptr(), 8, 64, 2048, 128)
+    assert lib.ns_w4_linear_ws(*small, None, 0, None) == 0
+    torch.cuda.synchronize()
 
 
 def test_gemv_ksplit_graph(kernels, oracle):
-    """The K-split M = 8 GEMV under graph capture: on a stream that already ran it eagerly (its
-    workspace exists) every replay equals the eager result bit for bit, with eager calls between
-    replays; on a fresh stream capture runs the unsplit kernel, still within the oracle's
-    tolerance."""
+    """The M = 8 GEMV at K = 18944 under graph capture, split (with a workspace) and in one pass
+    (ns_w4_linear): on a fresh stream each replay equals the eager call of the same entry
+    point bit for bit, with eager calls of other shapes between replays."""
     N, K, G, M = 1024, 18944, 128, 8
     Wq, S = synth.weights(N, K, G, seed=91)
     X = synth.activations(M, K, seed=92, per_row_seed=True)
     ref = oracle.linear_f64(X, Wq, S, G)
     xd, wd, sd = to_dev(X, torch.bfloat16), to_dev(Wq, torch.int32), to_dev(S, torch.bfloat16)
-    for warm in (True, False):
+    work = kernels.w4_linear_workspace(M, N, K, G)
+    for w in (work, None):
+        eager = kernels.w4_linear(xd, wd, sd, G, work=w)
+        torch.cuda.synchronize()
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            eager = kernels.w4_linear(xd, wd, sd, G) if warm else None
-        torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=s):
-            y = kernels.w4_linear(xd, wd, sd, G)
+            y = kernels.w4_linear(xd, wd, sd, G, work=w)
         for _ in range(3):
             g.replay()
             torch.cuda.synchronize()
             got = synth.bf16_bits_to_f32(to_host_bits(y)).astype(np.float64)
             check_bf16_faithful(got, ref, 2e-5)
-            if warm:
-                assert torch.equal(y, eager)
-                with torch.cuda.stream(s):
-                    kernels.w4_linear(xd[:3], wd, sd, G)
-                torch.cuda.synchronize()
+            assert torch.equal(y, eager)
+            kernels.w4_linear(xd[:3], wd, sd, G)
+            torch.cuda.synchronize()
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 6, 7, 8])
