@@ -451,35 +451,32 @@ def main():
         return ref
 
     def packed_sets():
-        """The same M = 1 and M = 8 sets on the packed tile format (ns_w4_repack once, then
-        ns_w4_linear_packed) for the layers with K <= 4096, where the packed kernel keeps the
-        activation in registers; the down layer (K = 18944) runs ns_w4_linear in the set."""
+        """The config-3 set (M = 8) on the packed tile format: ns_w4_repack once, then
+        ns_w4_linear_packed for every layer (K <= 4096: activation in registers; the down
+        projection, K = 18944, through the long-row kernel's LDS chunks), per layer and as a
+        set, beside the standard format's config-3 set. The packed format is the batched-decode
+        format (M = 2..16); at M = 1 ns_w4_linear_packed is not offered (the standard kernel is
+        faster there)."""
         pk = {name: [kern.w4_repack(wq, s, G) for wq, s in dev_w[name]] for name, _, _ in layers}
         torch.cuda.synchronize()
         res = {}
-        for M, xs in ((1, x1), (8, x8)):
-            ok = {name: K <= 4096 for name, N, K in layers}
+        M, xs = 8, x8
 
-            def run(i, which=None, M=M, xs=xs, ok=ok):
-                for name, N, K in layers:
-                    if which is not None and name != which:
-                        continue
-                    if ok[name]:
-                        kern.w4_linear_packed(xs[name], *pk[name][i % copies], N, G)
-                    else:
-                        kern.w4_linear(xs[name], *dev_w[name][i % copies], G)
-
+        def run(i, which=None):
             for name, N, K in layers:
-                g = graph_of(lambda i, name=name: run(i, which=name), n_launch)
-                ms = steady_ms(g, n_launch)
-                b = synth.gemv_bytes(M, N, K, G)
-                res[f"{name}_m{M}"] = {"us": round(ms * 1e3, 3), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
-                                       "packed": ok[name]}
-            g = graph_of(lambda i: run(i), 4 * copies)
-            ms = steady_ms(g, 4 * copies)
-            b = sum(synth.gemv_bytes(M, N, K, G) for _, N, K in layers)
-            res[f"set_m{M}"] = {"us": round(ms * 1e3, 3), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
-                                "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+                if which is None or name == which:
+                    kern.w4_linear_packed(xs[name], *pk[name][i % copies], N, G)
+
+        for name, N, K in layers:
+            g = graph_of(lambda i, name=name: run(i, which=name), n_launch)
+            ms = steady_ms(g, n_launch)
+            b = synth.gemv_bytes(M, N, K, G)
+            res[f"{name}_m{M}"] = {"us": round(ms * 1e3, 3), "gbs": round(b / (ms * 1e-3) / 1e9, 1)}
+        g = graph_of(lambda i: run(i), 4 * copies)
+        ms = steady_ms(g, 4 * copies)
+        b = sum(synth.gemv_bytes(M, N, K, G) for _, N, K in layers)
+        res[f"set_m{M}"] = {"us": round(ms * 1e3, 3), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
+                            "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         del pk
         torch.cuda.empty_cache()
         return res

@@ -35,6 +35,15 @@ namespace {
 
 constexpr uint32_t kPackOOB = 0x7fffffc0u;
 
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>), in order
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
 // One packed word -> eight bf16 (128 + q) in natural k order.
 __device__ __forceinline__ u32x4_t unpack_packed(uint32_t w) {
   u32x4_t d;
@@ -178,105 +187,125 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_packed_kernel(
   }
 }
 
-// Long rows (K > 32 * 128): the activation's group slices do not fit in registers, so the
-// activation rows (M of them) live in LDS, xl[c][m][128], each lane reading its A fragment of a
-// tile there (lanes of rows >= M use zeros, no LDS read); the -136 sum(x) corrections are
-// computed once per group with the same MFMA as the register kernel and kept in LDS, ct[c][16].
-// A wave issues all its tiles of a tile-row at once (a long row gives each wave GW of them),
-// which is the memory-level parallelism a 16-row tile-row of a long row needs.
+// Long rows (K > 32 * 128): the activation's group slices do not fit in registers. Each wave
+// still owns the k-groups c = wave, wave + NW, ... and issues all its tiles of a tile-row at once
+// (a long row gives each wave up to GW of them: the memory-level parallelism a 16-row tile-row of
+// a long row needs), but the activation passes through LDS in chunks: chunk g holds the k-groups
+// NW g .. NW g + NW - 1 of all M rows, xl[c % NW][m][128], so each wave finds its g-th group there.
+// Chunk g + 1 is loaded into registers while chunk g is used (two barriers per chunk); lanes of
+// activation rows >= M use zeros. The -136 sum(x) correction of a group is the same MFMA against a
+// constant -136 operand as in the register kernel, taken when the group's chunk is in LDS. Any
+// M <= 16 and K <= 128 NW GW fit: the LDS holds one chunk (M NW 256 bytes).
 template <int NW, int GW>
 __global__ __launch_bounds__(NW * kWave) void w4_gemv_packed_lds_kernel(
     const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wp,
     const uint16_t* __restrict__ Sp, uint16_t* __restrict__ Y, int M, int N, int K) {
   __shared__ float part[2][NW][256];
   extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int NT_ = NW * kWave;
   const int C = K >> 7;
   const int NT = (N + 15) >> 4;
-  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);                              // [C][M][128]
-  float* ct = reinterpret_cast<float*>(smem + (size_t)C * M * 256);              // [C][16]
+  uint16_t* xl = reinterpret_cast<uint16_t*>(smem);  // [NW][M][128]: one chunk of k-groups
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15, kg = lane >> 4;
   const int ng = wv < C ? (C - 1 - wv) / NW + 1 : 0;
+  const int nch = (C + NW - 1) / NW;  // chunks (uniform)
 
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(Wp), (short)0, (int)((size_t)NT * C * 1024), 0x00020000);
   const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(Sp), (short)0, (int)((size_t)NT * C * 32), 0x00020000);
-  u32x4_t wr[GW];
-  uint32_t sr[GW];
-  auto issue = [&](int t) {
+  // the activation through its own range-checked buffer: vectors past M K read as zeros
+  const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(X), (short)0, (int)((size_t)M * K * 2), 0x00020000);
+  // this wave's tile of chunk g into ring slot g % PD (PD tiles in flight per wave)
+  constexpr int PD = 3;
+  u32x4_t wr[PD];
+  uint32_t sr[PD];
+  auto issue = [&](int t, auto g_c) {
+    constexpr int g = decltype(g_c)::value;
+    const bool live = t < NT && g < ng;
+    const uint32_t tile = (uint32_t)(t * C + wv + NW * g);
+    wr[g % PD] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 wres, 16u * lane, live ? 1024u * tile : kPackOOB, kStreamAux));
+    sr[g % PD] = __builtin_amdgcn_raw_buffer_load_b16(sres, 2u * j, live ? 32u * tile : kPackOOB, kStreamAux);
+  };
+  // chunk g: vector e of the chunk (16 bytes) is row m = (e / 16) % M of k-group
+  // NW g + e / (16 M), k = 8 (e % 16) of the group; at most 4 vectors per thread (M <= 16)
+  const int cvec = M * NW * 16;
+  // per vector slot i of this thread: its k-group within a chunk (cl, or C when the slot is
+  // unused) and its byte offset in chunk 0; chunk g adds 256 NW g bytes
+  int xcl[4];
+  uint32_t xoff[4];
 #pragma unroll
-    for (int g = 0; g < GW; ++g) {
-      const bool live = t < NT && g < ng;
-      const uint32_t tile = (uint32_t)(t * C + wv + NW * g);
-      wr[g] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                              wres, 16u * lane, live ? 1024u * tile : kPackOOB, kStreamAux));
-      sr[g] = __builtin_amdgcn_raw_buffer_load_b16(sres, 2u * j, live ? 32u * tile : kPackOOB, kStreamAux);
+  for (int i = 0; i < 4; ++i) {
+    const int e = tid + i * NT_;
+    const int cl = e / (M * 16), m = (e >> 4) % M;
+    xcl[i] = e < cvec ? cl : C;
+    xoff[i] = 2u * (uint32_t)(m * K + 128 * cl + 8 * (e & 15));
+  }
+  auto load_chunk = [&](int g, u32x4_t (&v)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = NW * g + xcl[i] < C;
+      const uint32_t off = ok ? xoff[i] + 256u * (uint32_t)(NW * g) : kPackOOB;
+      v[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0));
     }
   };
-
-  // activation rows into LDS (their loads go out before the first tile-row's weights)
-  const int nvec = C * M * 16;
-  const u32x4_t* x4 = reinterpret_cast<const u32x4_t*>(X);
-  u32x4_t xv[4];
+  auto store_chunk = [&](const u32x4_t (&v)[4]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tid + i * NW * kWave;
-    const int c = e / (M * 16), m = (e / 16) % M, v = e % 16;
-    xv[i] = e < nvec ? x4[(size_t)m * (K >> 3) + 16 * c + v] : u32x4_t{0u, 0u, 0u, 0u};
-  }
-  int t = blockIdx.x;
-  issue(t);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int e = tid + i * NW * kWave;
-    if (e < nvec) *reinterpret_cast<u32x4_t*>(&xl[8 * e]) = xv[i];
-  }
-  for (int e = tid + 4 * NW * kWave; e < nvec; e += NW * kWave) {
-    const int c = e / (M * 16), m = (e / 16) % M, v = e % 16;
-    *reinterpret_cast<u32x4_t*>(&xl[8 * e]) = x4[(size_t)m * (K >> 3) + 16 * c + v];
-  }
-  __syncthreads();
-  auto afrag = [&](int c, int s4) {
-    return j < M ? *reinterpret_cast<const u32x4_t*>(&xl[((size_t)c * M + j) * 128 + 32 * s4 + 8 * kg])
+    for (int i = 0; i < 4; ++i) {
+      const int e = tid + i * NT_;
+      if (e < cvec) *reinterpret_cast<u32x4_t*>(&xl[8 * e]) = v[i];
+    }
+  };
+  auto afrag = [&](int s4) {  // this wave's group of the chunk in LDS
+    return j < M ? *reinterpret_cast<const u32x4_t*>(&xl[((size_t)wv * M + j) * 128 + 32 * s4 + 8 * kg])
                  : u32x4_t{0u, 0u, 0u, 0u};
   };
   const u32x4_t kNeg136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
-  for (int g = 0; g < ng; ++g) {
-    const int c = wv + NW * g;
-    f32x4_t d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4)
-      d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, afrag(c, s4)),
-                                                  __builtin_bit_cast(bf16x8_t, kNeg136), d, 0, 0, 0);
-    if (j == 0) *reinterpret_cast<f32x4_t*>(&ct[16 * c + 4 * kg]) = d;
-  }
-  __syncthreads();
 
-  for (int it = 0; t < NT; ++it, t += gridDim.x) {
-    if (it > 0) issue(t);
+  for (int it = 0, t = blockIdx.x; t < NT; ++it, t += gridDim.x) {
+    u32x4_t xv[4];
+    load_chunk(0, xv);  // ahead of the weights: the first chunk is needed first
+    issue(t, std::integral_constant<int, 0>{});
+    issue(t, std::integral_constant<int, 1>{});
+    issue(t, std::integral_constant<int, 2>{});
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    static_for<GW>([&](auto g_c) {
+      constexpr int g = decltype(g_c)::value;
+      if (g < nch) {  // uniform
+        lds_sync();   // every wave is done with the previous chunk
+        store_chunk(xv);
+        lds_sync();
+        if (g + 1 < nch) load_chunk(g + 1, xv);
+        if (g < ng) {
+          f32x4_t d = {0.f, 0.f, 0.f, 0.f};
+          u32x4_t xf[4];
 #pragma unroll
-    for (int g = 0; g < GW; ++g) {
-      if (g < ng) {
-        const int c = wv + NW * g;
-        f32x4_t d = *reinterpret_cast<const f32x4_t*>(&ct[16 * c + 4 * kg]);
+          for (int s4 = 0; s4 < 4; ++s4) {
+            xf[s4] = afrag(s4);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xf[s4]),
+                                                        __builtin_bit_cast(bf16x8_t, kNeg136), d, 0, 0, 0);
+          }
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4)
-          d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8_t, afrag(c, s4)),
-              __builtin_bit_cast(bf16x8_t, unpack_packed(wr[g][s4])), d, 0, 0, 0);
-        const float sc = bf16_bits_to_f32(sr[g] & 0xffffu);
+          for (int s4 = 0; s4 < 4; ++s4)
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                __builtin_bit_cast(bf16x8_t, xf[s4]),
+                __builtin_bit_cast(bf16x8_t, unpack_packed(wr[g % PD][s4])), d, 0, 0, 0);
+          const float sc = bf16_bits_to_f32(sr[g % PD] & 0xffffu);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc, d[r], acc[r]);
+          for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc, d[r], acc[r]);
+        }
+        if constexpr (g + PD < GW) issue(t, std::integral_constant<int, g + PD>{});
       }
-    }
+    });
     float* pw = &part[it & 1][wv][0];
 #pragma unroll
     for (int r = 0; r < 4; ++r) pw[(4 * kg + r) * 16 + j] = acc[r];
     __syncthreads();
-    for (int o = tid; o < 16 * M; o += NW * kWave) {
+    for (int o = tid; o < 16 * M; o += NT_) {
       const int i = o >> 4, jj = o & 15;
       float v = 0.f;
 #pragma unroll
@@ -287,7 +316,8 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_packed_lds_kernel(
   }
 }
 
-size_t packed_lds_bytes(int K, int M) { return (size_t)(K / 128) * M * 256 + (size_t)(K / 128) * 64; }
+// dynamic LDS of the long-row kernel: one chunk of NW k-groups of the M activation rows
+size_t packed_lds_bytes(int NW, int M) { return (size_t)NW * M * 256; }
 
 template <int NW, int GW>
 hipError_t launch_packed_lds(const uint16_t* X, const uint32_t* Wp, const uint16_t* Sp,
@@ -301,7 +331,7 @@ hipError_t launch_packed_lds(const uint16_t* X, const uint32_t* Wp, const uint16
   const int NT = (N + 15) / 16;
   const int grid = NT < cus ? NT : cus;
   hipLaunchKernelGGL((w4_gemv_packed_lds_kernel<NW, GW>), dim3(grid), dim3(NW * kWave),
-                     packed_lds_bytes(K, M), st, X, Wp, Sp, Y, M, N, K);
+                     packed_lds_bytes(NW, M), st, X, Wp, Sp, Y, M, N, K);
   return hipSuccess;
 }
 
@@ -349,7 +379,10 @@ int ns_w4_repack(const void* Wq, const void* S, void* Wp, void* Sp, int N, int K
 
 int ns_w4_linear_packed(const void* X, const void* Wp, const void* Sp, void* Y, int M, int N,
                         int K, int G, void* stream) {
-  if (M <= 0 || M > 16 || N <= 0 || K <= 0 || G != 128 || K % 128) return -2;
+  // M = 1 is not taken: the standard format's M = 1 kernel (ns_w4_linear) streams the same
+  // bytes faster (MI355X, Qwen2.5-7B layers: gate/up 13.8 against 15.2 us, q/k/v 4.7 against
+  // 5.1), so the packed format serves batched decode, M = 2..16, where it is the faster one
+  if (M < 2 || M > 16 || N <= 0 || K <= 0 || G != 128 || K % 128) return -2;
   if (ns::packed_weight_bytes(N, K) >= (1ull << 31)) return -2;
   if (!X || !Wp || !Sp || !Y || !ns::aligned(X, 16) || !ns::aligned(Wp, 16) ||
       !ns::aligned(Sp, 16) || !ns::aligned(Y, 2))
@@ -365,7 +398,7 @@ int ns_w4_linear_packed(const void* X, const void* Wp, const void* Sp, void* Y, 
     e = ns::launch_packed<16, 1>(x, wp, sp, y, M, N, K, st);
   else if (C <= 32)
     e = ns::launch_packed<16, 2>(x, wp, sp, y, M, N, K, st);
-  else if (C <= 160 && ns::packed_lds_bytes(K, M) <= 96 * 1024)
+  else if (C <= 160)
     e = ns::launch_packed_lds<16, 10>(x, wp, sp, y, M, N, K, st);
   else
     return -2;

@@ -304,9 +304,9 @@ def test_packed_entry_points_reject_bad_arguments(k):
     assert k.lib.ns_w4_repack(P, P, P + 8, P, 64, 256, 128, None) == -2
     assert k.lib.ns_w4_linear_packed(P, P, P, P, 17, 64, 256, 128, None) == -2   # M > 16
     assert k.lib.ns_w4_linear_packed(P, P, P, P, 0, 64, 256, 128, None) == -2
-    assert k.lib.ns_w4_linear_packed(P, P, P, P, 1, 64, 20608, 128, None) == -2  # K > 20480
-    assert k.lib.ns_w4_linear_packed(P, P, P, P, 8, 64, 18944, 128, None) == -2  # LDS budget
-    assert k.lib.ns_w4_linear_packed(P + 8, P, P, P, 1, 64, 256, 128, None) == -2
+    assert k.lib.ns_w4_linear_packed(P, P, P, P, 2, 64, 20608, 128, None) == -2  # K > 20480
+    assert k.lib.ns_w4_linear_packed(P, P, P, P, 1, 64, 256, 128, None) == -2    # M = 1: ns_w4_linear
+    assert k.lib.ns_w4_linear_packed(P + 8, P, P, P, 2, 64, 256, 128, None) == -2
 
 
 def test_gptq_workspace_and_rejects(k):
