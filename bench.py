@@ -175,31 +175,6 @@ def main():
                 break
         return statistics.median(time_graph(g) for _ in range(rounds)) / n
 
-    wall_khz = kern.wall_clock_khz()
-    clk0 = torch.zeros(32, dtype=torch.int64, device=dev)
-    clk1 = torch.zeros(32, dtype=torch.int64, device=dev)
-
-    def clock_mhz(fn, n):
-        """Average core clock (MHz) over the n launches of fn, replayed warm: ns_probe_clock before
-        and after them in one graph; the median over the XCDs both probes reached."""
-        def body(i):
-            if i == 0:
-                kern.probe_clock(clk0)
-            fn(i)
-            if i == n - 1:
-                kern.probe_clock(clk1)
-        g = graph_of(body, n)
-        steady_ms(g, n, rounds=1)
-        clk0.fill_(-1)
-        clk1.fill_(-1)
-        g.replay()
-        torch.cuda.synchronize()
-        a, b = clk0.view(16, 2).cpu().tolist(), clk1.view(16, 2).cpu().tolist()
-        per_xcd = [(t1 - t0) / (w1 - w0) * wall_khz / 1e3 for (t0, w0), (t1, w1) in zip(a, b)
-                   if min(t0, w0, t1, w1) >= 0 and w1 > w0]
-        del g
-        return round(statistics.median(per_xcd), 1) if per_xcd else None
-
     def deq_f32(wq, s):
         """Plain-torch fp32 dequantization on the GPU (the reference's CPU loop restated,
         bench/bench_w4a16.cu:156-173): nibble i of word j is k = 8j + i, w = (q - 8) * s."""
@@ -527,11 +502,10 @@ def main():
         value = bytes_m1 / (ms_step * 1e-3) / 1e9
 
     # ---------------- dominant kernel: gate+up GEMV, M=1, back-to-back launches, timed warm
-    # (steady_ms) with the core clock of the same launches recorded beside it
+    # (steady_ms)
     n_launch = 4 * copies
     g_gu = graph_of(lambda i: step(x1, i, which="gate_up"), n_launch)
     ms_gu = steady_ms(g_gu, n_launch)
-    mhz_gu = clock_mhz(lambda i: step(x1, i, which="gate_up"), n_launch)
     N_gu, K_gu = [(N, K) for n, N, K in layers if n == "gate_up"][0]
     bytes_gu = synth.gemv_bytes(1, N_gu, K_gu, G)
     achieved = bytes_gu / (ms_gu * 1e-3) / 1e9
@@ -540,7 +514,6 @@ def main():
                 "traffic": profiled_traffic(TRAFFIC_PROFILE),
                 "kernel": "w4_gemv_m1_kernel<7, 2, 16, 0, 0, 4, true> (gate_up 37888x3584, M=1)",
                 "bytes_per_launch": bytes_gu, "avg_launch_us": round(ms_gu * 1e3, 3),
-                "core_clock_mhz": mhz_gu,
                 "timing": "hip events on the launch stream around graph replays of "
                           f"{n_launch} launches on rotating weight copies, after >= 20 ms of "
                           "warm replays; median of 7"}

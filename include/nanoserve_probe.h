@@ -34,24 +34,6 @@ int ns_probe_read(const void* p, size_t bytes, void* sink, int grid, int waves, 
 int ns_probe_empty(int grid, int threads, void* stream);
 
 /*
- * No counterpart in the reference: one launch (64 single-wave workgroups, reaching every XCD)
- * that stores, per XCD x (the XCC_ID hardware register, 0..15), that XCD's shader-clock counter
- * (s_memtime, core clock cycles) and the constant-rate wall clock (s_memrealtime) as two uint64
- * at out[2x], out[2x + 1]: 32 uint64 in all; slots of absent XCDs are left as they were. Two
- * calls into two buffers bracketing other launches on one stream give their average core clock
- * on XCD x: (t1 - t0) / (w1 - w0) * ns_probe_wall_clock_khz (the counters of different XCDs
- * are not synchronised, so only slots written by both calls are compared). Returns -2 for NULL
- * or an `out` that is not 8-byte aligned.
- */
-int ns_probe_clock(void* out, void* stream);
-
-/*
- * The current device's wall-clock rate in kHz (hipDeviceAttributeWallClockRate) in *khz.
- * Returns -2 for NULL, else the hipError_t of the query.
- */
-int ns_probe_wall_clock_khz(int* khz);
-
-/*
  * The reference's benchmark times back-to-back launches on one stream from its C++ host loop
  * (bench/bench_w4a16.cu:42-78); this is that loop for bench.py: ns_w4_linear(X[i], Wq[i],
  * S[i], Y[i], M[i], N[i], K[i], G, stream) for i = 0 .. ncalls - 1, in order, with no host

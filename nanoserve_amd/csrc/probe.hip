@@ -14,8 +14,6 @@
 namespace ns {
 namespace {
 
-constexpr unsigned kClockSlots = 16;  // XCC_ID is a 4-bit field
-
 // Wave w of the grid reads 1 KiB blocks w, w + W, w + 2W, ... (W = waves in the grid), DEPTH
 // loads in flight per wave: the wave issues DEPTH loads, then folds them into a checksum. Blocks
 // past the end read through the buffer's range check (zeros, no memory traffic). The checksum is
@@ -46,23 +44,6 @@ __global__ __launch_bounds__(1024) void probe_read_kernel(const uint32_t* __rest
 
 __global__ void probe_empty_kernel() {}
 
-// Each workgroup records its XCD's shader-clock counter (s_memtime, counting core clock cycles)
-// and the constant-rate wall clock (s_memrealtime) into that XCD's slot (XCC_ID hardware
-// register), with a vector store. The counters of different XCDs are not synchronised, so two
-// launches bracketing other work give that work's average core clock per XCD from the slots
-// both launches wrote: d(memtime) / d(memrealtime) * wall-clock rate. The grid (64 workgroups)
-// reaches every XCD; workgroups sharing an XCD write the same slot with readings of the same
-// counters taken within the launch.
-__global__ void probe_clock_kernel(unsigned long long* __restrict__ out) {
-  const unsigned long long t = __builtin_amdgcn_s_memtime();
-  const unsigned long long w = __builtin_amdgcn_s_memrealtime();
-  // s_getreg_b32 hwreg(HW_REG_XCC_ID, 0, 4): id 20, offset 0, size 4 -> (3 << 11) | 20
-  const unsigned xcc = __builtin_amdgcn_s_getreg(6164) & (kClockSlots - 1);
-  if (threadIdx.x == 0) {
-    out[2 * xcc] = t;
-    out[2 * xcc + 1] = w;
-  }
-}
 }  // namespace
 }  // namespace ns
 
@@ -91,21 +72,6 @@ int ns_probe_empty(int grid, int threads, void* stream) {
   hipLaunchKernelGGL(ns::probe_empty_kernel, dim3(grid), dim3(threads), 0,
                      static_cast<hipStream_t>(stream));
   return static_cast<int>(hipGetLastError());
-}
-
-int ns_probe_clock(void* out, void* stream) {
-  if (!out || (reinterpret_cast<uintptr_t>(out) & 7)) return -2;
-  hipLaunchKernelGGL(ns::probe_clock_kernel, dim3(64), dim3(64), 0,
-                     static_cast<hipStream_t>(stream), static_cast<unsigned long long*>(out));
-  return static_cast<int>(hipGetLastError());
-}
-
-int ns_probe_wall_clock_khz(int* khz) {
-  if (!khz) return -2;
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e == hipSuccess) e = hipDeviceGetAttribute(khz, hipDeviceAttributeWallClockRate, dev);
-  return static_cast<int>(e);
 }
 
 int ns_probe_linear_loop(const void* const* X, const void* const* Wq, const void* const* S,

@@ -48,8 +48,6 @@ SIGNATURES["ns_decode_attention_noalloc"] = [_VP, _VP, _VP, _VP, _VP, _I32, _I32
 SIGNATURES["ns_probe_read"] = [_VP, _SZ, _VP, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_probe_empty"] = [_I32, _I32, _VP]
 SIGNATURES["ns_probe_linear_loop"] = [_VP] * 7 + [_I32, _I32, _VP]
-SIGNATURES["ns_probe_clock"] = [_VP, _VP]
-SIGNATURES["ns_probe_wall_clock_khz"] = [ctypes.POINTER(ctypes.c_int)]
 RESTYPES = {"ns_decode_attention_workspace": _SZ, "ns_w4_gptq_workspace": _SZ,
             "ns_w4_linear_workspace": _SZ}
 
@@ -517,21 +515,6 @@ class Kernels:
     def probe_empty(self, grid=1, threads=64):
         """Launch an empty kernel (the per-launch floor of a graph of kernels)."""
         self._check(self.lib.ns_probe_empty(grid, threads, self._stream()), "ns_probe_empty")
-
-    def probe_clock(self, out):
-        """Store each XCD's (shader-clock cycles, wall-clock ticks) into ``out`` (a contiguous
-        GPU int64 tensor of 32 elements: XCD x in out[2x], out[2x + 1]) from one launch on the
-        current stream (include/nanoserve_probe.h)."""
-        _require_gpu_tensor(out, "out", torch.int64)
-        if out.numel() != 32 or not out.is_contiguous():
-            raise ValueError("out must be a contiguous int64 tensor of 32 elements")
-        self._check(self.lib.ns_probe_clock(out.data_ptr(), self._stream()), "ns_probe_clock")
-
-    def wall_clock_khz(self):
-        """The current device's wall-clock rate in kHz (the tick rate probe_clock records)."""
-        v = ctypes.c_int(0)
-        self._check(self.lib.ns_probe_wall_clock_khz(ctypes.byref(v)), "ns_probe_wall_clock_khz")
-        return v.value
 
     def linear_loop(self, calls, group=128):
         """Issue ns_w4_linear for each (x, Wq, S, y) of ``calls`` back to back from the C++ host

@@ -40,7 +40,7 @@ def test_header_declares_the_reference_entry_points():
         "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn", "ns_decode_embed",
         "ns_bf16_gemv", "ns_w4_gptq_workspace", "ns_w4_gptq", "ns_w4_linear_swiglu",
         "ns_probe_read", "ns_probe_empty", "ns_probe_linear_loop", "ns_decode_attention_noalloc",
-        "ns_w4_linear_workspace", "ns_w4_linear_ws", "ns_probe_clock", "ns_probe_wall_clock_khz"])
+        "ns_w4_linear_workspace", "ns_w4_linear_ws"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -174,9 +174,6 @@ def test_linear_workspace_sizes_and_rejects(k):
     # shapes ns_w4_linear rejects are rejected the same way, workspace or not
     assert call(P, P, P, P, 9, 64, 18944, 128, P, need, None) == -2
     assert call(P, P, P, P, 8, 64, 18944, 100, P, need, None) == -2
-    assert k.lib.ns_probe_clock(None, None) == -2
-    assert k.lib.ns_probe_clock(P + 4, None) == -2
-    assert k.lib.ns_probe_wall_clock_khz(None) == -2
 
 
 def test_decode_attention_workspace_and_rejects(k):
