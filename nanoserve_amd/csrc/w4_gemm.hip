@@ -615,7 +615,7 @@ struct TileCfg {
   float eff;  // relative per-tile efficiency used by the planner
 };
 constexpr TileCfg kCfgs[] = {
-    {256, 256, 1.00f},  // 0: v1, BM 256, 4 waves x 64 cols
+    {256, 256, 1.00f},  // 0: v1, BM 256, 4 waves x 64 cols (not offered: spills)
     {256, 128, 0.90f},  // 1: v1, BM 256, 4 waves x 32 cols
     {128, 256, 0.85f},  // 2: v1, BM 128, 4 waves x 64 cols
     {128, 128, 0.75f},  // 3: v1, BM 128, 4 waves x 32 cols
@@ -671,9 +671,12 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
     }
     return GemmPlan{c, kCfgs[c].bm, kCfgs[c].bn};
   }
-  int best = 0;
+  // register-staged fallback (K % 64 == 32, or a group size that is not a power of two):
+  // plans 1..3; plan 0 (256 x 256 tiles, 64-column waves) needs more than the 512 registers a
+  // lane has at one wave per SIMD and spills, so it is not offered
+  int best = 1;
   double best_cost = 1e300;
-  for (int c = 0; c < 4; ++c) {
+  for (int c = 1; c < 4; ++c) {
     const long tiles = (long)((M + kCfgs[c].bm - 1) / kCfgs[c].bm) * ((N + kCfgs[c].bn - 1) / kCfgs[c].bn);
     const long rounds = (tiles + cus - 1) / cus;
     const double cost = (double)rounds * kCfgs[c].bm * kCfgs[c].bn / kCfgs[c].eff;
@@ -693,10 +696,6 @@ constexpr int kWeightAhead = 3;
 hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
   const dim3 grid((a.N + p.bn - 1) / p.bn, (a.M + p.bm - 1) / p.bm);
   switch (p.cfg) {
-    case 0:
-      hipLaunchKernelGGL((w4_gemm_kernel<256, 64, 4>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
-                         a.C, a.M, a.N, a.K, a.G);
-      return hipSuccess;
     case 1:
       hipLaunchKernelGGL((w4_gemm_kernel<256, 32, 4>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
                          a.C, a.M, a.N, a.K, a.G);

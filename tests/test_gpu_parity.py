@@ -312,8 +312,12 @@ def test_gemv_shapes_and_groups(kernels, oracle, N, K, G):
 
 
 @pytest.mark.parametrize("M,N,K,G", [(128, 128, 128, 128), (256, 384, 1024, 128),
-                                     (384, 256, 544, 32), (128, 640, 2048, 256)])
+                                     (384, 256, 544, 32), (128, 640, 2048, 256),
+                                     (512, 1024, 1056, 32), (512, 768, 1152, 96)])
 def test_gemm_small(kernels, oracle, M, N, K, G):
+    """Small GEMMs, including the register-staged fallback plans (K % 64 == 32: K = 544, 1056;
+    a group size that is not a power of two: G = 96) on grids large enough for its biggest
+    tiles."""
     Wq, S = synth.weights(N, K, G, seed=M + K)
     X = synth.activations(M, K, seed=N)
     y = run_linear(kernels, X, Wq, S, G)
