@@ -512,7 +512,7 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": profiled_traffic(TRAFFIC_PROFILE),
-                "kernel": "w4_gemv_m1_kernel<7, 2, 16, 0, 0, 4, true> (gate_up 37888x3584, M=1)",
+                "kernel": "w4_gemv_m1_kernel<7, 2, 16, 0, 0, 4, true, false> (gate_up 37888x3584, M=1)",
                 "bytes_per_launch": bytes_gu, "avg_launch_us": round(ms_gu * 1e3, 3),
                 "timing": "hip events on the launch stream around graph replays of "
                           f"{n_launch} launches on rotating weight copies, after >= 20 ms of "
