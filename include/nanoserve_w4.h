@@ -68,11 +68,14 @@ size_t ns_w4_linear_workspace(int M, int N, int K, int G);
 
 /*
  * No counterpart in the reference. ns_w4_linear with a caller-provided workspace for the K
- * split of the M = 2..8 decode GEMV (long rows, e.g. the 7B down projection K = 18944): the
- * slices write fp32 partials [ks][M][N] to `work` and a second launch sums them in slice order
- * and rounds to bf16. Same arithmetic and tolerance as ns_w4_linear, deterministic, but another
- * fp32 summation order (outputs may differ from ns_w4_linear's by one bf16 ulp). Shapes whose
- * ns_w4_linear_workspace is 0 run exactly as ns_w4_linear (work may then be NULL).
+ * split of the M = 2..8 decode GEMV (long rows, e.g. K = 11008 or 18944): the slices write
+ * fp32 partials [ks][M][N] to `work` and a second launch sums them in slice order and rounds
+ * to bf16. Same arithmetic and tolerance as ns_w4_linear, deterministic, but another fp32
+ * summation order (outputs may differ from ns_w4_linear's by one bf16 ulp). Shapes whose
+ * ns_w4_linear_workspace is 0 run exactly as ns_w4_linear (work may then be NULL); so do the
+ * shapes that both entry points run in one pass with the activation streamed through LDS
+ * (M >= 6 with about one 16-row group per compute unit, e.g. the 7B down projection at M = 8
+ * on MI355X), which leave the workspace unused.
  * Returns -2 when the shape needs a workspace and work is NULL, not 16-byte aligned or smaller
  * than ns_w4_linear_workspace(M, N, K, G); otherwise as ns_w4_linear. Calls that overlap in
  * time need workspaces of their own.

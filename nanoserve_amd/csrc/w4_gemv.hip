@@ -1268,6 +1268,179 @@ size_t m8_bytes(int nw, int cw, int gt) {
   return (size_t)nw * cw * kWave * 16 + (size_t)2 * nw * gt * (gt > 2 ? 32 : kWave) * 16;
 }
 
+// M = 2..8 with long rows (more than 32 pairs): the half-pair MFMA of w4_gemv_m8_kernel with the
+// activation streamed through LDS instead of held in registers, in one launch and without a
+// workspace.
+//  * 16 waves per workgroup, persistent over groups of two 8-row tiles (16 rows). K runs in
+//    chunks of 16 pairs (4096 k); wave w takes pair w of every chunk, for both tiles: two 1 KiB
+//    blocks per chunk, sharing one set of activation fragments and one -136 * sum_k x
+//    initialiser (four MFMAs against a constant operand).
+//  * Each chunk's activation (8 rows x 16 pairs x 512 B = 64 KiB; rows m >= M and pairs past
+//    K read as zeros) is loaded by the whole workgroup, four 16-byte pieces per thread, one
+//    chunk ahead, and stored in pair order into one of two LDS buffers. Within a pair, the
+//    16-byte unit of (piece e' = 4 kq + s of a half, row-half mh = 2 m + h) sits at
+//    16 e' + ((mh + e') mod 16): the 16 lanes of a fragment read (fixed e', every mh) and
+//    the 16 lanes of a staging store (fixed mh, every e') each cover all 64 banks once.
+//  * The weight blocks stream through a four-slot register ring two chunks ahead (it
+//    continues into the next group). One barrier per chunk publishes the next chunk's buffer;
+//    each wave's per-tile partials go to a compact LDS table at a group's last chunk, and two
+//    waves sum them over waves and halves after that chunk's barrier. A group's activation is
+//    read once per workgroup from L2 (each workgroup serves about one group on the 7B down
+//    projection), against once per wave and pair in registers before any weight block in
+//    the register kernel.
+__global__ __launch_bounds__(1024) void w4_gemv_m8c_kernel(
+    const uint16_t* __restrict__ X, const uint32_t* __restrict__ Wq,
+    const uint16_t* __restrict__ S, uint16_t* __restrict__ Y, int M, int N, int K) {
+  constexpr uint32_t kOOB = 0x7fffffc0u;
+  constexpr int NW = 16, PC = 16, GT = 2, R = 4;
+  extern __shared__ __align__(16) unsigned char smem[];
+  u32x4_t* xl = reinterpret_cast<u32x4_t*>(smem);                           // [2][PC][256]
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(smem + (size_t)2 * PC * 4096);  // [NW][GT][32]
+
+  const int P = K >> 8, C = K >> 7;
+  const int nch = (P + PC - 1) / PC;  // >= 3 (the planner sends K > 8192 only)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, kq = lane >> 4;
+  const int ntiles = (N + 7) >> 3;
+  const int ngroups = (ntiles + GT - 1) / GT;
+  const int gstep = (int)gridDim.x;
+  const uint32_t RB = (uint32_t)(K >> 1);
+
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(Wq), (short)0, (int)((size_t)N * RB), 0x00020000);
+  const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(S), (short)0, (int)((size_t)N * C * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(X), (short)0, (int)((size_t)M * K * 2), 0x00020000);
+
+  // staging: piece q = tid + 1024 i of a chunk is 16-byte piece e = q % 32 of row m = (q / 32)
+  // % 8 of pair pl = q / 256 (= wv / 4 + 4 i: uniform across the wave)
+  const int se = tid & 31, sm = (tid >> 5) & 7;
+  const uint32_t sxo = sm < M ? ((uint32_t)sm * (uint32_t)K + 8u * se) * 2u : kOOB;
+  const int sunit = 16 * (se & 15) + (((2 * sm + (se >> 4)) + (se & 15)) & 15);
+  u32x4_t xv[4];
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = PC * c + (wv >> 2) + 4 * i;
+      xv[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                              xres, sxo, p < P ? 512u * (uint32_t)p : kOOB, 0));
+    }
+  };
+  auto store_chunk = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      xl[(buf * PC + (wv >> 2) + 4 * i) * 256 + sunit] = pair_order(xv[i]);
+  };
+
+  // weight lane (j = (row nl, half hc), kq): row nl of the tile, bytes 64 hc + 16 kq of a pair
+  const int nl = c16 & 7, hc = c16 >> 3;
+  const uint32_t vw = (uint32_t)nl * RB + 64u * hc + 16u * kq;
+  const uint32_t vs = ((uint32_t)nl * (uint32_t)C + hc) * 2u;
+  // block (group g, chunk c, tile u): pair p = 16 c + wv of rows 8 (2 g + u) ..
+  auto issue = [&](u32x4_t& w, uint32_t& sc, int g, int c, int u) {
+    const int p = PC * c + wv;
+    const bool live = g < ngroups && p < P;
+    const uint32_t row0 = 8u * (uint32_t)(GT * g + u);
+    w = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                        wres, vw, live ? row0 * RB + 128u * p : kOOB, kStreamAux));
+    sc = __builtin_amdgcn_raw_buffer_load_b16(
+        sres, vs, live ? (row0 * (uint32_t)C + 2u * p) * 2u : kOOB, kStreamAux);
+  };
+
+  // fragment reads: lane (i = (m, h), kq), step s: unit 16 e' + ((mh + e') mod 16), e' = 4 kq + s
+  const int mh = 2 * (c16 & 7) + (c16 >> 3);
+  const u32x4_t kNeg136 = {0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u};
+  uint32_t vmask;
+  asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(vmask));
+  const uint32_t sbits = 0x43004300u;
+  const bool useful = (kq >> 1) == hc;
+  const int slot = (8 * hc + nl) * 2 + (kq & 1);
+
+  int g = (int)blockIdx.x;
+  // the first chunk's activation ahead of the weight ring (loads complete in issue order)
+  load_chunk(0);
+  u32x4_t ring[R];
+  uint32_t rsc[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) issue(ring[i], rsc[i], g, i >> 1, i & 1);
+  __builtin_amdgcn_sched_barrier(0);
+  store_chunk(0);
+  lds_sync();
+
+  f32x4_t acc[GT];
+  // chunk c of group g in LDS buffer PAR (ring slots 2 PAR, 2 PAR + 1)
+  auto chunk = [&](auto par, int c) {
+    constexpr int PAR = decltype(par)::value;
+    const bool last = c + 1 == nch;
+    // next chunk's activation (the next group's first chunk after a group's last)
+    const bool more = !last || g + gstep < ngroups;
+    if (more) load_chunk(last ? 0 : c + 1);
+    u32x4_t xa[4];
+    f32x4_t d0 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int e = 4 * kq + s;
+      xa[s] = xl[(PAR * PC + wv) * 256 + 16 * e + ((mh + e) & 15)];
+      d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[s]), as_bf16x8(kNeg136), d0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < GT; ++u) {
+      constexpr int kSlot0 = 2 * PAR;
+      f32x4_t d = d0;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(xa[s]), as_bf16x8(unpack_word_paired(ring[kSlot0 + u][s], vmask, sbits)), d, 0, 0, 0);
+      const float sc = bf16_bits_to_f32(rsc[kSlot0 + u] & 0xffffu);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[u][r] = __builtin_fmaf(sc, d[r], acc[u][r]);
+      __builtin_amdgcn_sched_barrier(0);
+      // refill with the block two chunks ahead (into the next group past the last chunk)
+      if (c + 2 < nch)
+        issue(ring[kSlot0 + u], rsc[kSlot0 + u], g, c + 2, u);
+      else
+        issue(ring[kSlot0 + u], rsc[kSlot0 + u], g + gstep, c + 2 - nch, u);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (last && useful) {
+#pragma unroll
+      for (int u = 0; u < GT; ++u) red[(wv * GT + u) * 32 + slot] = acc[u];
+    }
+    if (more) store_chunk(1 - PAR);
+    lds_sync();
+  };
+
+  int cc = 0;  // chunks done by this workgroup: its parity picks the buffer and ring slots
+  for (; g < ngroups; g += gstep) {
+#pragma unroll
+    for (int u = 0; u < GT; ++u) acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < nch; ++c, ++cc) {
+      if (cc & 1)
+        chunk(std::integral_constant<int, 1>{}, c);
+      else
+        chunk(std::integral_constant<int, 0>{}, c);
+    }
+    // output (m = lane / 8, row nl = lane % 8) of tile u: half h of every wave sits at slot
+    // (8 h + nl) * 2 + m / 4, register m % 4. The table is rewritten only at this
+    // workgroup's next group's last chunk, nch >= 3 barriers later.
+    if (wv < GT) {
+      const int u = wv, om = lane >> 3, on = lane & 7;
+      const int q0 = 4 * (2 * on + (om >> 2)) + (om & 3), q1 = q0 + 4 * 16;
+      float v = 0.f;
+      for (int w = 0; w < NW; ++w) {
+        const float* pw = reinterpret_cast<const float*>(red + (w * GT + u) * 32);
+        v += pw[q0] + pw[q1];
+      }
+      const int n = 8 * (GT * g + u) + on;
+      if (om < M && n < N) Y[(size_t)om * N + n] = (uint16_t)f32_to_bf16_rne(v);
+    }
+  }
+}
+
+constexpr size_t kM8cBytes = (size_t)2 * 16 * 4096 + (size_t)16 * 2 * 32 * 16;
+
 // Generic fallback: one wavefront per output row, exact fp32 dequant, fp32 FMA.
 template <int MMAX>
 __global__ __launch_bounds__(256) void w4_gemv_generic_kernel(
@@ -1429,6 +1602,21 @@ hipError_t launch_m8(const GemvArgs& a, int nw, int cap, const M8Split& sp, hipS
     hipLaunchKernelGGL(w4_gemv_m8_merge_kernel, dim3((mn + 255) / 256), dim3(256), 0, st, sp.part,
                        a.Y, mn, sp.ks);
   }
+  return hipSuccess;
+}
+
+// The chunked-activation M = 2..8 kernel: one workgroup per CU at most, each over 16-row
+// groups.
+hipError_t launch_m8c(const GemvArgs& a, hipStream_t st) {
+  const void* fn = reinterpret_cast<const void*>(&w4_gemv_m8c_kernel);
+  hipError_t e = cached_max_dynamic_lds(fn, (int)kM8cBytes);
+  if (e != hipSuccess) return e;
+  int cus = 0;
+  e = cached_cu_count(&cus);
+  if (e != hipSuccess) return e;
+  const int ngroups = ((a.N + 7) / 8 + 1) / 2;
+  hipLaunchKernelGGL(w4_gemv_m8c_kernel, dim3(max(1, min(ngroups, cus))), dim3(1024), kM8cBytes, st,
+                     a.X, a.Wq, a.S, a.Y, a.M, a.N, a.K);
   return hipSuccess;
 }
 
@@ -1649,6 +1837,20 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st, flo
     return fc7 ? launch_m1<7, 2, 8>(a, st, fz, L.wpc) : launch_m1<8, 2, 8>(a, st, fz, L.wpc);
   }
   if (p.m8) {
+    // Long rows at M >= 6 with about one 16-row group per CU (the 7B down projection at
+    // M = 8: 224 groups): the chunked-activation kernel, one launch, no workspace. On MI355X
+    // (interleaved A/B, us, M = 8 / M = 4): 3584 x 18944 15.9 / 15.3 against 16.6 / 15.4 in K
+    // slices and 18.6 / 15.8 unsplit; 4096 x 14336 13.5 / 12.9 against 14.6 / 13.2 and 15.2 /
+    // 12.5. With two or more groups per workgroup (8192 x 11008: 18.6 against 16.9 unsplit)
+    // or fewer groups than three quarters of the CUs (2048 x 11008: 10.2 against 8.7 split)
+    // and at M = 2 (15.0 against 14.2 unsplit) it is slower, so those keep the other plans.
+    if (p.ks > 1 && a.M >= 6) {
+      int cus = 0;
+      const hipError_t e = cached_cu_count(&cus);
+      if (e != hipSuccess) return e;
+      const int groups = ((a.N + 7) / 8 + 1) / 2;
+      if (4 * groups >= 3 * cus && groups <= cus) return launch_m8c(a, st);
+    }
     // the K split runs only in the caller's workspace (ns_w4_linear_ws); ns_w4_linear passes
     // none and runs every shape unsplit
     M8Split sp;

@@ -198,7 +198,7 @@ class Kernels:
         of 128, as the reference does. ``out`` (not in the reference): a contiguous [M, N]
         bf16 tensor to write instead of a new one, for M that needs no padding. ``work`` (not in
         the reference): a workspace from ``w4_linear_workspace``; with it the M = 2..8 GEMV
-        splits long rows over K (ns_w4_linear_ws), without it every shape runs unsplit
+        may split long rows over K (ns_w4_linear_ws), without it no shape is split
         (ns_w4_linear)."""
         _require_gpu_tensor(x, "x", torch.bfloat16)
         _require_gpu_tensor(Wq, "Wq", torch.int32)

@@ -240,6 +240,58 @@ def test_gemv_ksplit_graph(kernels, oracle):
             torch.cuda.synchronize()
 
 
+# Long rows at M >= 6 with about one 16-row group per compute unit (3/4 to 1 of the CUs; on
+# MI355X's 256 CUs, N from 3072 to 4096) run the chunked-activation kernel through both entry
+# points: chunks of 4096 k whose last one is partial (K = 8448: 33 pairs, a one-pair last
+# chunk; K = 12544: 49 pairs), ragged N (3590: the last tile cut, an odd tile count), and the
+# largest K (20480).
+M8C_SHAPES = [(3590, 8448, (6, 8)), (3104, 12544, (7,)), (4096, 20480, (8,)), (3584, 18944, (6, 8))]
+
+
+@pytest.mark.parametrize("N,K,Ms", M8C_SHAPES)
+def test_gemv_m8_chunked(kernels, oracle, N, K, Ms):
+    """Within half a bf16 ulp (+2e-5 ||ref||) of the oracle; ns_w4_linear and ns_w4_linear_ws
+    give the same bits (one kernel, the workspace unused), and a graph replay on a fresh stream
+    repeats the eager call bit for bit."""
+    G = 128
+    Wq, S = synth.weights(N, K, G, seed=N + 5 * K)
+    wd, sd = to_dev(Wq, torch.int32), to_dev(S, torch.bfloat16)
+    work = kernels.w4_linear_workspace(max(Ms), N, K, G)
+    for M in Ms:
+        X = synth.activations(M, K, seed=M + 50, per_row_seed=True)
+        xd = to_dev(X, torch.bfloat16)
+        ref = oracle.linear_f64(X, Wq, S, G)
+        y = kernels.w4_linear(xd, wd, sd, G)
+        yw = kernels.w4_linear(xd, wd, sd, G, work=work)
+        torch.cuda.synchronize()
+        check_bf16_faithful(synth.bf16_bits_to_f32(to_host_bits(y)).astype(np.float64), ref, 2e-5)
+        assert torch.equal(y, yw)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            yg = kernels.w4_linear(xd, wd, sd, G)
+        for _ in range(2):
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(yg, y)
+            kernels.w4_linear(xd[:2], wd, sd, G)
+            torch.cuda.synchronize()
+
+
+def test_gemv_m8_chunked_dequant_bitexact(kernels, oracle):
+    """The chunked kernel returns each dequantized weight bit for bit: every k of the first and
+    last 256, both sides of each chunk boundary, and a seeded sample in between."""
+    N, K = 3584, 8448
+    rng = np.random.default_rng(17)
+    edge = set(range(256)) | set(range(K - 256, K))
+    for b in (4096, 8192):
+        edge |= set(range(b - 16, b + 16))
+    mid = rng.choice(np.arange(256, K - 256), 96, replace=False)
+    _onehot_probe(kernels, oracle, N=N, K=K, G=128, M=8, staged=False, seed=23,
+                  ks=sorted(edge | set(int(k) for k in mid)))
+
+
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_gemv_every_m(kernels, oracle, M):
     N, K, G = 200, 1024, 128       # N not a multiple of 16: row-tile tail
