@@ -1778,8 +1778,10 @@ GemvPlan gemv_plan(int M, int N, int K, int G) {
   // M = 2..8 with whole rows of a 16-row group in LDS (K <= 4096): weights staged in LDS.
   p.lds = M >= 2 && G == 128 && C <= 32 && small_buf;
   if (p.lds) {
-    p.nw = C <= 16 ? 8 : 14;
-    p.rt = C <= 28 ? 2 : 3;  // chunks per wave (covers C with nw waves)
+    // waves and chunks per wave covering C (sixteen waves of two chunks past 28 chunks: three
+    // chunks per wave spilled registers)
+    p.nw = C <= 16 ? 8 : C <= 28 ? 14 : 16;
+    p.rt = 2;
     return p;
   }
   p.rt = 1;
@@ -1871,9 +1873,9 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st, flo
   }
   if (p.lds) {
     // copies per wave per group: 16 rows x ceil(C / 16) row pieces + the scale slab
-    if (p.nw == 8 && p.rt == 2) return launch_lds<8, 8, 2, 3, 3>(a, st, 1);
-    if (p.nw == 14 && p.rt == 2) return launch_lds<8, 14, 2, 3, 3>(a, st, 1);
-    if (p.nw == 14 && p.rt == 3) return launch_lds<8, 14, 3, 3, 3>(a, st, 1);
+    if (p.nw == 8) return launch_lds<8, 8, 2, 3, 3>(a, st, 1);
+    if (p.nw == 14) return launch_lds<8, 14, 2, 3, 3>(a, st, 1);
+    if (p.nw == 16) return launch_lds<8, 16, 2, 3, 3>(a, st, 1);
     return hipErrorInvalidValue;
   }
   if (p.xlds) {

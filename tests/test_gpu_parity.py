@@ -341,6 +341,18 @@ def test_gemv_small_batch_pair_counts(kernels, oracle, M, N, K):
     check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
 
 
+@pytest.mark.parametrize("M", [2, 5, 8])
+@pytest.mark.parametrize("N,K", [(200, 384), (300, 1920), (1000, 3712), (72, 3968)])
+def test_gemv_small_batch_odd_chunks(kernels, oracle, M, N, K):
+    """M = 2..8 with an odd number of 128-k chunks (K not a multiple of 256, up to 32 chunks):
+    the kernel that stages each 16-row group's weights in LDS, with 8, 14 and 16 waves."""
+    G = 128
+    Wq, S = synth.weights(N, K, G, seed=N + 7 * K + M)
+    X = synth.activations(M, K, seed=K + 2 * M, per_row_seed=True)
+    y = run_linear(kernels, X, Wq, S, G)
+    check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
+
+
 @pytest.mark.parametrize("M,N,K", [(3, 4600, 3584), (7, 37880, 3584), (4, 3580, 3584), (6, 3577, 18944),
                                    (8, 9000, 7168)])
 def test_gemv_small_batch_group_heights(kernels, oracle, M, N, K):
