@@ -1577,7 +1577,7 @@ int m8_per_cu(int nw, hipError_t* err) {
 }
 
 // K slices of the M = 2..8 kernel: ks workgroups share each group, each writing its fp32
-// partials to the stream's split workspace ([ks][M][N]); a merge launch sums them into Y.
+// partials to the caller's workspace ([ks][M][N]); a merge launch sums them into Y.
 struct M8Split {
   int ks = 1;
   float* part = nullptr;

@@ -38,7 +38,8 @@ struct GemvPlan {
 
 bool gemv_fast_path_ok(int M, int N, int K, int G);
 GemvPlan gemv_plan(int M, int N, int K, int G);
-// ws / ws_bytes: the K-split workspace (gemv_split_bytes); nullptr runs every shape unsplit.
+// ws / ws_bytes: the K-split workspace (gemv_split_bytes); nullptr splits no shape (shapes the
+// chunked-activation kernel serves run in one pass either way).
 hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st,
                        float* ws = nullptr, size_t ws_bytes = 0);
 
