@@ -70,6 +70,9 @@ def parse():
                    help="only the config-2 set (the four layers at M=1), e.g. under a profiler")
     p.add_argument("--m8-only", action="store_true",
                    help="only the config-3 set (the four layers at M=8), e.g. under a profiler")
+    p.add_argument("--packed-only", action="store_true",
+                   help="only the packed-format launches (config-3 set and config-4 GEMMs), e.g. "
+                        "under a profiler")
     p.add_argument("--decode-only", action="store_true",
                    help="only the config-5 decode step (28-layer W4 Qwen2.5-7B, context 1024)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -426,12 +429,13 @@ def main():
         return ref
 
     def packed_sets():
-        """The config-3 set (M = 8) on the packed tile format: ns_w4_repack once, then
-        ns_w4_linear_packed for every layer (K <= 4096: activation in registers; the down
-        projection, K = 18944, through the long-row kernel's LDS chunks), per layer and as a
-        set, beside the standard format's config-3 set. The packed format is the batched-decode
-        format (M = 2..16); at M = 1 ns_w4_linear_packed is not offered (the standard kernel is
-        faster there)."""
+        """The config-3 set (M = 8) and the config-4 GEMMs on the packed tile format:
+        ns_w4_repack once, then ns_w4_linear_packed for every layer (K <= 4096: activation in
+        registers; the down projection, K = 18944, through the long-row kernel's LDS chunks),
+        per layer and as a set, beside the standard format's config-3 set, and the prefill
+        GEMMs (M > 16) beside config4_gemm. The packed format serves batched decode (M = 2..16)
+        and prefill; at M = 1 ns_w4_linear_packed is not offered (the standard kernel is faster
+        there)."""
         pk = {name: [kern.w4_repack(wq, s, G) for wq, s in dev_w[name]] for name, _, _ in layers}
         torch.cuda.synchronize()
         res = {}
@@ -442,9 +446,10 @@ def main():
                 if which is None or name == which:
                     kern.w4_linear_packed(xs[name], *pk[name][i % copies], N, G)
 
+        nl = 4 * copies  # launches per timed graph, as the per-layer legs
         for name, N, K in layers:
-            g = graph_of(lambda i, name=name: run(i, which=name), n_launch)
-            ms = steady_ms(g, n_launch)
+            g = graph_of(lambda i, name=name: run(i, which=name), nl)
+            ms = steady_ms(g, nl)
             b = synth.gemv_bytes(M, N, K, G)
             res[f"{name}_m{M}"] = {"us": round(ms * 1e3, 3), "gbs": round(b / (ms * 1e-3) / 1e9, 1)}
         g = graph_of(lambda i: run(i), 4 * copies)
@@ -452,12 +457,29 @@ def main():
         b = sum(synth.gemv_bytes(M, N, K, G) for _, N, K in layers)
         res[f"set_m{M}"] = {"us": round(ms * 1e3, 3), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
                             "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        # the config-4 prefill GEMMs on the packed tiles (ns_w4_linear_packed at M > 16)
+        for name, N, K in layers:
+            if name not in ("gate_up", "down"):
+                continue
+            for Mg in (512, 2048):
+                xa = dev_bits(synth.activations(Mg, K, seed=Mg), torch.bfloat16)
+                reps = 6
+                g = graph_of(lambda i, name=name, xa=xa, N=N: kern.w4_linear_packed(
+                    xa, *pk[name][i % copies], N, G), reps)
+                ms = steady_ms(g, reps)
+                tf = synth.gemm_flops(Mg, N, K) / (ms * 1e-3) / 1e12
+                res[f"gemm_{name}_m{Mg}"] = {"us": round(ms * 1e3, 1), "tflops": round(tf, 1),
+                                             "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4)}
+                del xa
         del pk
         torch.cuda.empty_cache()
         return res
 
     if args.gemm_only:
         print(json.dumps({"config4_gemm": gemm_set()}), flush=True)
+        return
+    if args.packed_only:
+        print(json.dumps({"packed_format": packed_sets()}), flush=True)
         return
     if args.decode_only:
         print(json.dumps({"config5_decode": decode_step()}), flush=True)

@@ -97,14 +97,17 @@ int ns_w4_repack(const void* Wq, const void* S, void* Wp, void* Sp, int N, int K
                  void* stream);
 
 /*
- * No counterpart in the reference. ns_w4_linear for batched decode, M = 2..16, on packed weights
- * (ns_w4_repack): Y [M][N] bf16 (RNE) = X [M][K] bf16 . deq(W)^T with fp32 accumulation, the same
- * exact dequantisation and products as ns_w4_linear's decode GEMV (fp32 sums over k-groups in
- * another order: outputs agree with ns_w4_linear's to one bf16 ulp, most bit for bit). K up to
- * 20480 (longer rows pass the activation through LDS in chunks). M = 1 is not taken: there the
- * standard format's kernel (ns_w4_linear) is the faster one. Returns -2 for M outside 2..16,
- * G != 128, K % 128 != 0, K > 20480, a packed size of 2 GiB or more, NULL or misaligned pointers
- * (X, Wp, Sp 16-byte aligned).
+ * No counterpart in the reference. ns_w4_linear on packed weights (ns_w4_repack), for batched
+ * decode and prefill: Y [M][N] bf16 (RNE) = X [M][K] bf16 . deq(W)^T with fp32 accumulation.
+ * M = 2..16: the same exact dequantisation and products as ns_w4_linear's decode GEMV (fp32 sums
+ * over k-groups in another order: outputs agree with ns_w4_linear's to one bf16 ulp, most bit for
+ * bit); K up to 20480 (longer rows pass the activation through LDS in chunks). M > 16: the
+ * prefill GEMM on the packed tiles, with the reference GEMM's numerics (each weight staged as
+ * bf16_rne((q - 8) s) before the bf16 products, as ns_w4_linear's GEMM; another fp32 summation
+ * order, so outputs agree with ns_w4_linear's to one bf16 ulp); (M + 256) K * 2 below 2^31.
+ * M = 1 is not taken: there the standard format's kernel (ns_w4_linear) is the faster one.
+ * Returns -2 for M < 2, G != 128, K % 128 != 0, K > 20480 at M <= 16, an M > 16 past the size
+ * limit, a packed size of 2 GiB or more, NULL or misaligned pointers (X, Wp, Sp 16-byte aligned).
  */
 int ns_w4_linear_packed(const void* X, const void* Wp, const void* Sp, void* Y, int M, int N,
                         int K, int G, void* stream);

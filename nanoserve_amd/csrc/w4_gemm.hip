@@ -608,6 +608,254 @@ __global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 && KS == 1 ? 2 : 1) voi
     store_tile_direct<MI, NJ>(acc, C, M, N, m0, n0 + wv * WN);
 }
 
+// Packed tile format (ns_w4_repack: tiles of 16 rows x 128 k, lane l's 16 bytes = row l % 16 at
+// k = 32 s + 8 (l / 16) + e, word s, nibbles in the order e = 0 2 4 6 1 3 5 7) -> 8 staged weights
+// bf16_rne((q - 8) * s) in natural k order: with that nibble order the pairs (e0, e1), (e2, e3),
+// (e4, e5), (e6, e7) sit at bit offsets 0/16, 4/20, 8/24, 12/28, so each v_and_or_b32 of a
+// shifted word yields one fp16 pair (1024 + q) already in k order; the rest is dequant_word_bf16.
+__device__ __forceinline__ u32x4_t dequant_word_bf16_pk(uint32_t w, uint32_t vmask, float s,
+                                                        float ns1032) {
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  constexpr uint32_t kE1024 = 0x64006400u;
+  const h2_t h0 = __builtin_bit_cast(h2_t, and_or_s(w, vmask, kE1024));        // e0, e1
+  const h2_t h1 = __builtin_bit_cast(h2_t, and_or_s(w >> 4, vmask, kE1024));   // e2, e3
+  const h2_t h2 = __builtin_bit_cast(h2_t, and_or_s(w >> 8, vmask, kE1024));   // e4, e5
+  const h2_t h3 = __builtin_bit_cast(h2_t, and_or_s(w >> 12, vmask, kE1024));  // e6, e7
+  u32x4_t d;
+  d[0] = pack_bf16x2_rne(__builtin_fmaf((float)h0[0], s, ns1032), __builtin_fmaf((float)h0[1], s, ns1032));
+  d[1] = pack_bf16x2_rne(__builtin_fmaf((float)h1[0], s, ns1032), __builtin_fmaf((float)h1[1], s, ns1032));
+  d[2] = pack_bf16x2_rne(__builtin_fmaf((float)h2[0], s, ns1032), __builtin_fmaf((float)h2[1], s, ns1032));
+  d[3] = pack_bf16x2_rne(__builtin_fmaf((float)h3[0], s, ns1032), __builtin_fmaf((float)h3[1], s, ns1032));
+  return d;
+}
+
+// Prefill GEMM on the packed tile format (the pre-shuffled layout the reference's README:148-151
+// proposes for its GEMM): C[M][N] (bf16, RNE) = A[M][K] . deq(Wp, Sp)^T with the reference GEMM's
+// numerics (each weight staged as bf16_rne((q - 8) s), w4a16.cuh:190-198; fp32 accumulation).
+//  * v_mfma_f32_16x16x32_bf16: a packed tile's lane (j, kg) run is, word by word, exactly the
+//    B operand of lane (j, kg) for the tile's four 32-k steps, so one 16-byte load per lane per
+//    tile-row and 128 k feeds four steps (the standard layout needs one per 64 k), and the
+//    nibble order gives k-ordered fp16 pairs without a byte permute.
+//  * BM x 32 NWN output tiles, NWN waves of BM rows x 32 columns (two tile-rows) per K group:
+//    each staged weight word feeds BM / 16 MFMAs; 128 x 128 tiles run four workgroups per CU
+//    (64 accumulators per lane), the K-split plans one eight-wave workgroup per CU.
+//  * The activation tile (BM x 64 bf16 per stage, two stages per K group) comes in by
+//    buffer-to-LDS loads with the standard GEMM's XOR swizzle (16-byte chunk c of row r at
+//    c ^ (r / 2) % 8: the 16 rows of a fragment read hit distinct banks); 64-k block 2c + h uses
+//    words 2h, 2h + 1 of the lane's run of tile column c. The weights of a group's tile column
+//    WD steps ahead are issued at the step's first block into a register ring of WD + 1 slots.
+//  * KS > 1 (tile grids that do not fill the chip, e.g. the 7B down projection): KS groups of
+//    NWN waves split the tile columns (group g takes columns g, g + KS, ..., through its own
+//    two stages); groups 1 .. KS-1 then hand their accumulators to group 0 through LDS, one
+//    group per round, and group 0 adds them in group order.
+//  * Epilogue (group 0): each wave rounds its BM x 32 sub-tile to bf16 into a private part of
+//    the (then free) LDS ring and stores 16-byte row segments.
+template <int BM, int NWN, int KS, int WD>
+__global__ __launch_bounds__(NWN * KS * kWave, KS > 1 ? 1 : 4)
+void w4_gemm_pk_kernel(const uint16_t* __restrict__ A, const uint32_t* __restrict__ Wp,
+                       const uint16_t* __restrict__ Sp, uint16_t* __restrict__ C, int M, int N, int K) {
+  constexpr int NJ = 2, MI = BM / 16, BN = 32 * NWN, ST = 2;
+  constexpr int STAGE = BM * BK;          // bf16 elements per activation stage
+  constexpr int IPW = BM / (8 * NWN);     // 16-byte LDS-load instructions per wave per stage
+  static_assert(BM % (8 * NWN) == 0, "whole LDS-load instructions per wave");
+  constexpr int WR = WD + 1;              // weight ring slots (tile columns)
+  constexpr uint32_t kOOB = 0x7fffffc0u;
+  constexpr int RING = ST * KS * STAGE;                           // bf16 elements
+  constexpr int PART = KS > 1 ? NWN * kWave * MI * NJ * 4 * 2 : 0;  // one group's partials
+  static_assert(NWN * BM * 32 <= RING, "epilogue sub-tiles fit the ring");
+  __shared__ __align__(16) uint16_t As[RING > PART ? RING : PART];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wq = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wv = wq % NWN, ks = wq / NWN;  // column slice and K group of this wave
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int CT = K >> 7;                  // tile columns
+  const int T = (CT + KS - 1) / KS;       // steps (tile columns per group)
+  const int NT = (N + 15) >> 4;           // tile rows
+
+  const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(A), (short)0, (int)((size_t)M * K * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(Wp), (short)0, (int)((size_t)NT * CT * 1024), 0x00020000);
+  const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(Sp), (short)0, (int)((size_t)NT * CT * 32), 0x00020000);
+
+  uint32_t a_voff[IPW];
+#pragma unroll
+  for (int t = 0; t < IPW; ++t) {
+    const int row = 8 * (wv * IPW + t) + (lane >> 3);
+    const int ch = (lane & 7) ^ ((row >> 1) & 7);
+    a_voff[t] = ((uint32_t)(m0 + row) * (uint32_t)K + 8u * ch) * 2u;
+  }
+  // stage st of this group <- 64-k block kb (past K: zeros)
+  auto issue_a = [&](int st, int kb) {
+    const uint32_t so = kb < 2 * CT ? 128u * kb : kOOB;
+#pragma unroll
+    for (int t = 0; t < IPW; ++t)
+      lds_load16(ares, &As[(st * KS + ks) * STAGE + 512 * (wv * IPW + t)], a_voff[t], so);
+  };
+
+  // weights: lane (j, kg)'s 16-byte run of tile (tile-row n0 / 16 + 2 wv + jj, column c) and
+  // the scale of that tile's row j
+  uint32_t w_voff[NJ], s_voff[NJ];
+#pragma unroll
+  for (int jj = 0; jj < NJ; ++jj) {
+    const uint32_t tr = (uint32_t)((n0 >> 4) + NJ * wv + jj);
+    w_voff[jj] = tr * (uint32_t)CT * 1024u + 16u * lane;
+    s_voff[jj] = (tr * (uint32_t)CT * 16u + (uint32_t)(lane & 15)) * 2u;
+  }
+  struct WRegs {
+    u32x4_t w[NJ];
+    uint32_t s[NJ];
+  };
+  auto issue_w = [&](WRegs& r, int c) {
+    const bool live = c < CT;
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+      r.w[jj] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                wres, w_voff[jj], live ? 1024u * c : kOOB, 0));
+      r.s[jj] = __builtin_amdgcn_raw_buffer_load_b16(sres, s_voff[jj], live ? 32u * c : kOOB, 0);
+    }
+  };
+
+  f32x4_t acc[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) acc[i][jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  uint32_t vmask;
+  asm volatile("v_mov_b32 %0, 0x000F000F" : "=v"(vmask));
+  const int fr = lane & 15, kg = lane >> 4;
+  // one 64-k stage: two 32-k steps; step s2 reads chunk 4 s2 + kg of rows 16 i + fr
+  auto compute = [&](int st, const WRegs& r, auto half_c) {
+    constexpr int H = decltype(half_c)::value;
+    const uint16_t* as = &As[(st * KS + ks) * STAGE];
+    float sc[NJ], nb[NJ];
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+      sc[jj] = bf16_bits_to_f32(r.s[jj] & 0xffffu);
+      nb[jj] = -1032.f * sc[jj];
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      u32x4_t bfr[NJ];
+#pragma unroll
+      for (int jj = 0; jj < NJ; ++jj) bfr[jj] = dequant_word_bf16_pk(r.w[jj][2 * H + s2], vmask, sc[jj], nb[jj]);
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int row = 16 * i + fr;
+        const int ch = (4 * s2 + kg) ^ ((row >> 1) & 7);
+        const u32x4_t af = *reinterpret_cast<const u32x4_t*>(&as[row * BK + 8 * ch]);
+#pragma unroll
+        for (int jj = 0; jj < NJ; ++jj)
+          acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af), as_bf16x8(bfr[jj]), acc[i][jj], 0, 0, 0);
+      }
+    }
+  };
+
+  WRegs wr[WR];
+  // step t covers this group's tile column c = ks + KS t: blocks 2c (half 0) and 2c + 1 (half
+  // 1). The weights of the first WD steps go first, then the first activation stage (the
+  // per-block wait below counts only the weight loads issued after a block's stage)
+#pragma unroll
+  for (int p = 0; p < WD; ++p) issue_w(wr[p], ks + KS * p);
+  __builtin_amdgcn_sched_barrier(0);
+  issue_a(0, 2 * ks);
+  __builtin_amdgcn_sched_barrier(0);
+  constexpr int UNR = 2 * WR;  // blocks per period: every (stage, slot, half) combination
+  for (int b0 = 0; b0 < 2 * T; b0 += UNR) {
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int bi = b0 + u, t = bi >> 1;  // this group's block bi: step t, half u % 2
+      const int c = ks + KS * t;
+      // block bi's stage was issued in block bi - 1, followed by that block's weight loads when
+      // bi - 1 starts a step
+      if (u & 1)
+        wait_vmcnt_c<2 * NJ>();
+      else
+        wait_vmcnt_c<0>();
+      lds_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      // the next block of this group: the second half of column c, or the first of c + KS
+      issue_a((u + 1) % ST, (u & 1) ? 2 * (c + KS) : 2 * c + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if ((u & 1) == 0) issue_w(wr[(u / 2 + WD) % WR], c + KS * WD);
+      __builtin_amdgcn_sched_barrier(0);
+      if (c < CT) {
+        if (u & 1)
+          compute(u % ST, wr[(u / 2) % WR], std::integral_constant<int, 1>{});
+        else
+          compute(u % ST, wr[(u / 2) % WR], std::integral_constant<int, 0>{});
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  wait_vmcnt_c<0>();
+  lds_barrier();  // every wave is done with the ring
+
+  if constexpr (KS > 1) {
+    // group g hands its accumulators to group 0 in round g (lane-major: word r * 64 + lane of
+    // the wave's slice); group 0 adds them in group order
+    float* pb = reinterpret_cast<float*>(As) + wv * (kWave * MI * NJ * 4);
+#pragma unroll 1
+    for (int g = 1; g < KS; ++g) {
+      if (ks == g) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pb[((i * NJ + jj) * 4 + r) * kWave + lane] = acc[i][jj][r];
+      }
+      lds_barrier();
+      if (ks == 0) {
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][jj][r] += pb[((i * NJ + jj) * 4 + r) * kWave + lane];
+      }
+      lds_barrier();
+    }
+    if (ks != 0) return;  // no barrier follows
+  }
+
+  // epilogue: wave-private BM x 32 bf16 sub-tile at As + wv * BM * 32 (row stride 32), then
+  // 16-byte row segments; registers r, r + 1 are rows m, m + 1 of one column
+  uint16_t* lds = &As[wv * (BM * 32)];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+      for (int r = 0; r < 4; r += 2) {
+        const int row = 16 * i + 4 * kg + r;
+        const uint32_t pk = pack_bf16x2_rne(acc[i][jj][r], acc[i][jj][r + 1]);
+        lds[row * 32 + 16 * jj + fr] = (uint16_t)pk;
+        lds[(row + 1) * 32 + 16 * jj + fr] = (uint16_t)(pk >> 16);
+      }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's sub-tile is in LDS
+  const int n0w = n0 + 32 * wv;
+  const int cr = lane >> 2, cc = lane & 3;
+  // whole 16-byte segments when the tile is inside C and C's rows are 16-byte aligned
+  const bool full = m0 + BM <= M && n0w + 32 <= N && (N & 7) == 0 &&
+                    (reinterpret_cast<uintptr_t>(C) & 15) == 0;
+#pragma unroll
+  for (int p = 0; p < BM / 16; ++p) {
+    const int row = 16 * p + cr;
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&lds[row * 32 + 8 * cc]);
+    const int m = m0 + row, n = n0w + 8 * cc;
+    if (full) {
+      *reinterpret_cast<u32x4_t*>(&C[(size_t)m * N + n]) = v;
+    } else if (m < M) {
+      for (int e = 0; e < 8; ++e)
+        if (n + e < N) C[(size_t)m * N + n + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+}
+
 inline int ilog2(int g) { return 31 - __builtin_clz((unsigned)g); }
 
 struct TileCfg {
@@ -692,6 +940,47 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
 // (WD): 3 measured best on MI355X (gate/up M = 2048 537-541 -> 520-523 us, M = 512 159-161 ->
 // 153-157, down M = 2048 313 -> 308, against 1; 4 and 5 no better; same outputs bit for bit).
 constexpr int kWeightAhead = 3;
+
+// Tile plan of the packed-format GEMM (M > 16 through ns_w4_linear_packed). On MI355X (interleaved
+// A/B against the standard GEMM on the config-4 shapes, us): 128 x 128 tiles, four workgroups
+// per CU, by default (gate/up 37888 x 3584 at M = 512 135.1 against 152.5, at M = 2048 478.6
+// against 532.5; 256 x 128 tiles there 162.3 and 516.4); 256 x 128 tiles with K split over two
+// wave groups when those tiles fill three quarters to all of the CUs once and K >= 8192 (down
+// 3584 x 18944 at M = 2048: 261.1 against 283.5; 128 x 128 tiles 279.8); 128 x 64 tiles with K
+// split over four groups of two waves when 128 x 128 tiles leave CUs idle and the 128 x 64 ones
+// fill three quarters to all of them (down at M = 512: 98.3 against 100.4; 128 x 128 tiles
+// 212.6).
+int gemm_packed_plan(int M, int N, int K) {
+  int cus = 256;  // the device's CU count (a failed query leaves MI355X's; the launch reports it)
+  if (cached_cu_count(&cus) != hipSuccess || cus <= 0) cus = 256;
+  const long t256 = (long)((M + 255) / 256) * ((N + 127) / 128);
+  const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
+  const long t128x64 = (long)((M + 127) / 128) * ((N + 63) / 64);
+  if (t256 <= cus && 4 * t256 >= 3 * cus && K >= 8192) return 1;
+  if (t128 < cus && 4 * t128x64 >= 3 * cus && t128x64 <= cus) return 2;
+  return 0;
+}
+
+// The weights two tile columns (256 k) ahead of the activation stages in every plan.
+hipError_t launch_gemm_packed(const uint16_t* A, const uint32_t* Wp, const uint16_t* Sp, uint16_t* C,
+                              int M, int N, int K, int plan, hipStream_t st) {
+  switch (plan) {
+    case 0:  // 128 x 128 tiles
+      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 4, 1, 2>), dim3((N + 127) / 128, (M + 127) / 128),
+                         dim3(256), 0, st, A, Wp, Sp, C, M, N, K);
+      return hipSuccess;
+    case 1:  // 256 x 128 tiles, K split over two groups of four waves, one workgroup per CU
+      hipLaunchKernelGGL((w4_gemm_pk_kernel<256, 4, 2, 2>), dim3((N + 127) / 128, (M + 255) / 256),
+                         dim3(512), 0, st, A, Wp, Sp, C, M, N, K);
+      return hipSuccess;
+    case 2:  // 128 x 64 tiles, K split over four groups of two waves, one workgroup per CU
+      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 2, 4, 2>), dim3((N + 63) / 64, (M + 127) / 128),
+                         dim3(512), 0, st, A, Wp, Sp, C, M, N, K);
+      return hipSuccess;
+    default:
+      return hipErrorInvalidValue;
+  }
+}
 
 hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
   const dim3 grid((a.N + p.bn - 1) / p.bn, (a.M + p.bm - 1) / p.bm);

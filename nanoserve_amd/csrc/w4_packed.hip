@@ -381,8 +381,12 @@ int ns_w4_linear_packed(const void* X, const void* Wp, const void* Sp, void* Y, 
                         int K, int G, void* stream) {
   // M = 1 is not taken: the standard format's M = 1 kernel (ns_w4_linear) streams the same
   // bytes faster (MI355X, Qwen2.5-7B layers: gate/up 13.8 against 15.2 us, q/k/v 4.7 against
-  // 5.1), so the packed format serves batched decode, M = 2..16, where it is the faster one
-  if (M < 2 || M > 16 || N <= 0 || K <= 0 || G != 128 || K % 128) return -2;
+  // 5.1), so the packed format serves batched decode, M = 2..16, where it is the faster one,
+  // and prefill, M > 16
+  // M > 16 (prefill) runs the GEMM on the packed tiles: its activation offsets (rows up to M +
+  // 255 of the last tile) stay in 31 bits
+  if (M < 2 || N <= 0 || K <= 0 || G != 128 || K % 128) return -2;
+  if (M > 16 && (uint64_t)(M + 256) * (uint64_t)K * 2 >= (1ull << 31)) return -2;
   if (ns::packed_weight_bytes(N, K) >= (1ull << 31)) return -2;
   if (!X || !Wp || !Sp || !Y || !ns::aligned(X, 16) || !ns::aligned(Wp, 16) ||
       !ns::aligned(Sp, 16) || !ns::aligned(Y, 2))
@@ -394,7 +398,9 @@ int ns_w4_linear_packed(const void* X, const void* Wp, const void* Sp, void* Y, 
   const auto sp = static_cast<const uint16_t*>(Sp);
   const auto y = static_cast<uint16_t*>(Y);
   hipError_t e;
-  if (C <= 16)
+  if (M > 16)
+    e = ns::launch_gemm_packed(x, wp, sp, y, M, N, K, ns::gemm_packed_plan(M, N, K), st);
+  else if (C <= 16)
     e = ns::launch_packed<16, 1>(x, wp, sp, y, M, N, K, st);
   else if (C <= 32)
     e = ns::launch_packed<16, 2>(x, wp, sp, y, M, N, K, st);

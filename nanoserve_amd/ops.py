@@ -488,9 +488,10 @@ class Kernels:
         return Wp, Sp
 
     def w4_linear_packed(self, x, Wp, Sp, N, group=128, out=None):
-        """x [M, K] bf16 (batched decode, 2 <= M <= 16) -> y [M, N] bf16, as w4_linear on the
-        packed weights of w4_repack (agreeing with it to one bf16 ulp). M = 1 is rejected: the
-        standard format (w4_linear) is the faster one there."""
+        """x [M, K] bf16 (M >= 2: batched decode up to 16 rows, prefill beyond) -> y [M, N]
+        bf16, as w4_linear on the packed weights of w4_repack (agreeing with it to one bf16
+        ulp; M > 16 with the GEMM's bf16-staged weights, as w4_linear's GEMM). M = 1 is
+        rejected: the standard format (w4_linear) is the faster one there."""
         _require_gpu_tensor(x, "x", torch.bfloat16)
         _require_gpu_tensor(Wp, "Wp", torch.int32)
         _require_gpu_tensor(Sp, "Sp", torch.bfloat16)

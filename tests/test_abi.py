@@ -299,7 +299,8 @@ def test_packed_entry_points_reject_bad_arguments(k):
     assert k.lib.ns_w4_repack(P, P, P, P, 64, 256, 64, None) == -2      # G != 128
     assert k.lib.ns_w4_repack(P, P, P, P, 64, 200, 128, None) == -2     # K % 128
     assert k.lib.ns_w4_repack(P, P, P + 8, P, 64, 256, 128, None) == -2
-    assert k.lib.ns_w4_linear_packed(P, P, P, P, 17, 64, 256, 128, None) == -2   # M > 16
+    # M > 16 (the packed GEMM) past 31-bit activation offsets: (M + 256) K * 2 >= 2^31
+    assert k.lib.ns_w4_linear_packed(P, P, P, P, 17, 64, 3933184, 128, None) == -2
     assert k.lib.ns_w4_linear_packed(P, P, P, P, 0, 64, 256, 128, None) == -2
     assert k.lib.ns_w4_linear_packed(P, P, P, P, 2, 64, 20608, 128, None) == -2  # K > 20480
     assert k.lib.ns_w4_linear_packed(P, P, P, P, 1, 64, 256, 128, None) == -2    # M = 1: ns_w4_linear

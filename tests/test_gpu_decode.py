@@ -480,6 +480,84 @@ def test_w4_linear_packed_equals_w4_linear(k, N, K, M):
     close(y, ref64, rtol=2 ** -8, atol=1e-5 * ref64.abs().max().item())
 
 
+@pytest.mark.parametrize("M,N,K", [(17, 200, 1024), (129, 1000, 3584), (300, 264, 8448), (64, 40, 384),
+                                   (33, 4608, 3584), (256, 3584, 18944), (512, 4608, 3584)])
+def test_w4_linear_packed_gemm(k, M, N, K):
+    """M > 16 on packed weights runs the prefill GEMM on the packed tiles, with the reference
+    GEMM's numerics: within half a bf16 ulp (+1e-5 ||ref||) of the oracle's product with every
+    weight staged as bf16((q - 8) s) (shapes the float64 oracle finishes in seconds), and within
+    one bf16 ulp of ns_w4_linear's GEMM where that takes the shape (N % 128 == 0: the same staged
+    weights, fp32 sums in another order). Row tails inside a 256-row tile, column tails inside a
+    16-row tile-row and a 128-column tile, and K from 384 to 18944."""
+    print(f"w4_linear_packed gemm M={M} N={N} K={K}", flush=True)
+    Wq, S = _w4(N, K, seed=93)
+    Wp, Sp = k.w4_repack(Wq, S)
+    x = rnd(M, K, seed=94)
+    y = k.w4_linear_packed(x, Wp, Sp, N)
+    torch.cuda.synchronize()
+    if N % 128 == 0:
+        ref = k.w4_linear(x, Wq, S, 128)
+        torch.cuda.synchronize()
+        close(y, ref.double().cpu(), rtol=2 ** -7, atol=2e-5 * ref.abs().max().item())
+    if M * N * K <= 2 ** 30:
+        xb = x.cpu().view(torch.int16).numpy().view("uint16")
+        staged = torch.from_numpy(O.linear_f64(xb, Wq.cpu().numpy().view("uint32"),
+                                               S.cpu().view(torch.int16).numpy().view("uint16"),
+                                               128, bf16_weights=True))
+        close(y, staged, rtol=2 ** -8, atol=1e-5 * staged.abs().max().item())
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 3584, 8192), (1800, 3560, 8192), (512, 3584, 4096),
+                                   (400, 3500, 4096)])
+def test_w4_linear_packed_gemm_split_plans(k, M, N, K):
+    """The packed GEMM's K-split plans (on MI355X's 256 CUs: 256 x 128 tiles over two wave groups
+    for the first two shapes, 128 x 64 tiles over four for the last two), with ragged M and N:
+    within one bf16 ulp of ns_w4_linear's GEMM on the first N // 128 * 128 rows, and within half
+    an ulp (+1e-5 ||ref||) of the oracle's bf16-staged product on one activation row of every
+    128-row band (a different offset per band) over all N columns."""
+    print(f"w4_linear_packed gemm split M={M} N={N} K={K}", flush=True)
+    Wq, S = _w4(N, K, seed=97)
+    Wp, Sp = k.w4_repack(Wq, S)
+    x = rnd(M, K, seed=98)
+    y = k.w4_linear_packed(x, Wp, Sp, N)
+    N1 = N // 128 * 128
+    ref = k.w4_linear(x, Wq[:N1], S[:N1], 128)
+    torch.cuda.synchronize()
+    close(y[:, :N1], ref.double().cpu(), rtol=2 ** -7, atol=2e-5 * ref.abs().max().item())
+    rows = [min(M - 1, 128 * b + (37 * b) % 128) for b in range((M + 127) // 128)]
+    xb = x[rows].cpu().view(torch.int16).numpy().view("uint16")
+    staged = torch.from_numpy(O.linear_f64(xb, Wq.cpu().numpy().view("uint32"),
+                                           S.cpu().view(torch.int16).numpy().view("uint16"), 128,
+                                           bf16_weights=True))
+    close(y[rows], staged, rtol=2 ** -8, atol=1e-5 * staged.abs().max().item())
+
+
+def test_w4_linear_packed_gemm_graph_and_rows_past_tile(k):
+    """The packed GEMM under graph capture repeats the eager call bit for bit (eager calls of
+    other shapes between replays), and rows of a partial last tile leave the rows past M alone."""
+    N, K = 1000, 3584
+    Wq, S = _w4(N, K, seed=95)
+    Wp, Sp = k.w4_repack(Wq, S)
+    x = rnd(300, K, seed=96)
+    big = torch.full((320, N), 7.0, dtype=torch.bfloat16, device=DEV)
+    out = big[:300]
+    k.w4_linear_packed(x, Wp, Sp, N, out=out)
+    eager = out.clone()
+    torch.cuda.synchronize()
+    assert (big[300:] == 7.0).all()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        yg = k.w4_linear_packed(x, Wp, Sp, N)
+    for _ in range(2):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, eager)
+        k.w4_linear_packed(x[:20], Wp, Sp, N)
+        torch.cuda.synchronize()
+
+
 # ------------------------------------------------------------------ the runner
 def _hf_model(H, nh, nkv, I, V, layers, seed):
     pytest.importorskip("transformers")
