@@ -637,8 +637,8 @@ __device__ __forceinline__ u32x4_t dequant_word_bf16_pk(uint32_t w, uint32_t vma
 //    tile-row and 128 k feeds four steps (the standard layout needs one per 64 k), and the
 //    nibble order gives k-ordered fp16 pairs without a byte permute.
 //  * BM x 32 NWN output tiles, NWN waves of BM rows x 32 columns (two tile-rows) per K group:
-//    each staged weight word feeds BM / 16 MFMAs; 128 x 128 tiles run four workgroups per CU
-//    (64 accumulators per lane), the K-split plans one eight-wave workgroup per CU.
+//    each staged weight word feeds BM / 16 MFMAs; 128 x 128 tiles (64 accumulators per lane)
+//    run four four-wave workgroups per CU, or two eight-wave ones with K split over two groups.
 //  * The activation tile (BM x 64 bf16 per stage, two stages per K group) comes in by
 //    buffer-to-LDS loads with the standard GEMM's XOR swizzle (16-byte chunk c of row r at
 //    c ^ (r / 2) % 8: the 16 rows of a fragment read hit distinct banks); 64-k block 2c + h uses
@@ -662,8 +662,9 @@ void w4_gemm_pk_kernel(const uint16_t* __restrict__ A, const uint32_t* __restric
   constexpr uint32_t kOOB = 0x7fffffc0u;
   constexpr int RING = ST * KS * STAGE;                           // bf16 elements
   constexpr int PART = KS > 1 ? NWN * kWave * MI * NJ * 4 * 2 : 0;  // one group's partials
-  static_assert(NWN * BM * 32 <= RING, "epilogue sub-tiles fit the ring");
-  __shared__ __align__(16) uint16_t As[RING > PART ? RING : PART];
+  constexpr int EPI = NWN * BM * 32;                              // epilogue sub-tiles
+  constexpr int LDSN = RING > PART ? (RING > EPI ? RING : EPI) : (PART > EPI ? PART : EPI);
+  __shared__ __align__(16) uint16_t As[LDSN];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wq = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -942,39 +943,38 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
 constexpr int kWeightAhead = 3;
 
 // Tile plan of the packed-format GEMM (M > 16 through ns_w4_linear_packed). On MI355X (interleaved
-// A/B against the standard GEMM on the config-4 shapes, us): 128 x 128 tiles, four workgroups
-// per CU, by default (gate/up 37888 x 3584 at M = 512 135.1 against 152.5, at M = 2048 478.6
-// against 532.5; 256 x 128 tiles there 162.3 and 516.4); 256 x 128 tiles with K split over two
-// wave groups when those tiles fill three quarters to all of the CUs once and K >= 8192 (down
-// 3584 x 18944 at M = 2048: 261.1 against 283.5; 128 x 128 tiles 279.8); 128 x 64 tiles with K
-// split over four groups of two waves when 128 x 128 tiles leave CUs idle and the 128 x 64 ones
-// fill three quarters to all of them (down at M = 512: 98.3 against 100.4; 128 x 128 tiles
-// 212.6).
+// A/B runs on the config-4 shapes, us; the standard GEMM in brackets): 128 x 128 tiles, four
+// workgroups per CU, by default (gate/up 37888 x 3584 at M = 512 133.0 [152.2], at M = 2048 476.3
+// [530.8]); the same tiles with K split over two wave groups (one eight-wave workgroup per CU)
+// when K >= 8192 and the tiles make at most two rounds of the CUs (down 3584 x 18944 at M = 2048:
+// 266.2 [298.2], 300.5 unsplit, 284.4 for 256 x 128 tiles split the same way); 128 x 64 tiles
+// with K split over four groups of two waves when 128 x 128 tiles would leave CUs idle and the
+// 128 x 64 ones fill three quarters to all of them (down at M = 512: 98.8 [102.3], 189.8 for
+// 128 x 128 tiles). Weights one tile column (128 k) ahead in every plan: two columns ahead ran
+// 3-8 % slower (gate/up at M = 2048 489.6 against 473.0, M = 512 142.9 against 132.4), three 13 %.
 int gemm_packed_plan(int M, int N, int K) {
   int cus = 256;  // the device's CU count (a failed query leaves MI355X's; the launch reports it)
   if (cached_cu_count(&cus) != hipSuccess || cus <= 0) cus = 256;
-  const long t256 = (long)((M + 255) / 256) * ((N + 127) / 128);
   const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
   const long t128x64 = (long)((M + 127) / 128) * ((N + 63) / 64);
-  if (t256 <= cus && 4 * t256 >= 3 * cus && K >= 8192) return 1;
   if (t128 < cus && 4 * t128x64 >= 3 * cus && t128x64 <= cus) return 2;
+  if (K >= 8192 && t128 <= 2 * cus) return 1;
   return 0;
 }
 
-// The weights two tile columns (256 k) ahead of the activation stages in every plan.
 hipError_t launch_gemm_packed(const uint16_t* A, const uint32_t* Wp, const uint16_t* Sp, uint16_t* C,
                               int M, int N, int K, int plan, hipStream_t st) {
   switch (plan) {
     case 0:  // 128 x 128 tiles
-      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 4, 1, 2>), dim3((N + 127) / 128, (M + 127) / 128),
+      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 4, 1, 1>), dim3((N + 127) / 128, (M + 127) / 128),
                          dim3(256), 0, st, A, Wp, Sp, C, M, N, K);
       return hipSuccess;
-    case 1:  // 256 x 128 tiles, K split over two groups of four waves, one workgroup per CU
-      hipLaunchKernelGGL((w4_gemm_pk_kernel<256, 4, 2, 2>), dim3((N + 127) / 128, (M + 255) / 256),
+    case 1:  // 128 x 128 tiles, K split over two groups of four waves
+      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 4, 2, 1>), dim3((N + 127) / 128, (M + 127) / 128),
                          dim3(512), 0, st, A, Wp, Sp, C, M, N, K);
       return hipSuccess;
-    case 2:  // 128 x 64 tiles, K split over four groups of two waves, one workgroup per CU
-      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 2, 4, 2>), dim3((N + 63) / 64, (M + 127) / 128),
+    case 2:  // 128 x 64 tiles, K split over four groups of two waves
+      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 2, 4, 1>), dim3((N + 63) / 64, (M + 127) / 128),
                          dim3(512), 0, st, A, Wp, Sp, C, M, N, K);
       return hipSuccess;
     default:

@@ -510,7 +510,7 @@ def test_w4_linear_packed_gemm(k, M, N, K):
 @pytest.mark.parametrize("M,N,K", [(2048, 3584, 8192), (1800, 3560, 8192), (512, 3584, 4096),
                                    (400, 3500, 4096)])
 def test_w4_linear_packed_gemm_split_plans(k, M, N, K):
-    """The packed GEMM's K-split plans (on MI355X's 256 CUs: 256 x 128 tiles over two wave groups
+    """The packed GEMM's K-split plans (on MI355X's 256 CUs: 128 x 128 tiles over two wave groups
     for the first two shapes, 128 x 64 tiles over four for the last two), with ragged M and N:
     within one bf16 ulp of ns_w4_linear's GEMM on the first N // 128 * 128 rows, and within half
     an ulp (+1e-5 ||ref||) of the oracle's bf16-staged product on one activation row of every
