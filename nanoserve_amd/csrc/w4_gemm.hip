@@ -382,6 +382,36 @@ __device__ __forceinline__ void wait_vmcnt_c() {
 // 256-row tiles carry 128 accumulators per lane: the launch bound asks for two waves per SIMD
 // (two four-wave workgroups per CU, or one eight-wave workgroup with KS = 2) so the compiler
 // keeps them in VGPRs beside the operands.
+// K-split handoff of the GEMMs: group g hands its accumulators (MI x NJ vectors of R floats) to
+// group 0 in round g through pb (this wave's slice of the free LDS ring, lane-major: word r * 64
+// + lane); group 0 adds them in group order. Every wave of the workgroup calls it (it holds
+// barriers).
+template <int KS, int MI, int NJ, typename V>
+__device__ __forceinline__ void k_group_handoff(V (&acc)[MI][NJ], float* pb, int ks, int lane) {
+  constexpr int R = sizeof(V) / sizeof(float);
+#pragma unroll 1
+  for (int g = 1; g < KS; ++g) {
+    if (ks == g) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int r = 0; r < R; ++r) pb[((i * NJ + j) * R + r) * kWave + lane] = acc[i][j][r];
+    }
+    lds_barrier();
+    if (ks == 0) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int r = 0; r < R; ++r) acc[i][j][r] += pb[((i * NJ + j) * R + r) * kWave + lane];
+    }
+    lds_barrier();
+  }
+}
+
 template <int BM, int WN, int NWN, int ST, bool SW = false, int KS = 1, int WD = 1>
 __global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 && KS == 1 ? 2 : 1) void w4_gemm2_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ Wq,
@@ -574,30 +604,7 @@ __global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 && KS == 1 ? 2 : 1) voi
   wait_vmcnt_c<0>();  // the trailing out-of-range loads have landed before the LDS is reused
   lds_barrier();      // every wave is done reading the ring
   if constexpr (KS > 1) {
-    // group g hands its accumulators to group 0 in round g (lane-major: word r * 64 + lane of
-    // the wave's slice); group 0 adds them in group order
-    float* pb = reinterpret_cast<float*>(As) + wv * (kWave * MI * NJ * 16);
-#pragma unroll 1
-    for (int g = 1; g < KS; ++g) {
-      if (ks == g) {
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-          for (int j = 0; j < NJ; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) pb[((i * NJ + j) * 16 + r) * kWave + lane] = acc[i][j][r];
-      }
-      lds_barrier();
-      if (ks == 0) {
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-          for (int j = 0; j < NJ; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] += pb[((i * NJ + j) * 16 + r) * kWave + lane];
-      }
-      lds_barrier();
-    }
+    k_group_handoff<KS>(acc, reinterpret_cast<float*>(As) + wv * (kWave * MI * NJ * 16), ks, lane);
     if (ks != 0) return;  // no barrier follows
   }
   if constexpr (SW)
@@ -606,6 +613,43 @@ __global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 && KS == 1 ? 2 : 1) voi
     store_tile_lds<MI, NJ, ELS>(acc, &As[wv * BM * ELS], C, M, N, m0, n0 + wv * WN);
   else
     store_tile_direct<MI, NJ>(acc, C, M, N, m0, n0 + wv * WN);
+}
+
+// Epilogue of the 16x16x32 GEMMs: a wave's BM x 32 accumulators (16-row fragments i, 16-column
+// halves jj; registers r, r + 1 are rows m, m + 1 of one column) rounded to bf16 into its private
+// LDS sub-tile lds (row stride 32), then stored as 16-byte row segments of C (element by element
+// at the edges of C or when C's rows are not 16-byte aligned).
+template <int BM>
+__device__ __forceinline__ void store_tile_16x16(const f32x4_t (&acc)[BM / 16][2], uint16_t* lds,
+                                                 uint16_t* C, int M, int N, int m0, int n0w, int lane) {
+  const int fr = lane & 15, kg = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < BM / 16; ++i)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int r = 0; r < 4; r += 2) {
+        const int row = 16 * i + 4 * kg + r;
+        const uint32_t pk = pack_bf16x2_rne(acc[i][jj][r], acc[i][jj][r + 1]);
+        lds[row * 32 + 16 * jj + fr] = (uint16_t)pk;
+        lds[(row + 1) * 32 + 16 * jj + fr] = (uint16_t)(pk >> 16);
+      }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's sub-tile is in LDS
+  const int cr = lane >> 2, cc = lane & 3;
+  const bool full = m0 + BM <= M && n0w + 32 <= N && (N & 7) == 0 &&
+                    (reinterpret_cast<uintptr_t>(C) & 15) == 0;
+#pragma unroll
+  for (int p = 0; p < BM / 16; ++p) {
+    const int row = 16 * p + cr;
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&lds[row * 32 + 8 * cc]);
+    const int m = m0 + row, n = n0w + 8 * cc;
+    if (full) {
+      *reinterpret_cast<u32x4_t*>(&C[(size_t)m * N + n]) = v;
+    } else if (m < M) {
+      for (int e = 0; e < 8; ++e)
+        if (n + e < N) C[(size_t)m * N + n + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+    }
+  }
 }
 
 // Packed tile format (ns_w4_repack: tiles of 16 rows x 128 k, lane l's 16 bytes = row l % 16 at
@@ -796,65 +840,10 @@ void w4_gemm_pk_kernel(const uint16_t* __restrict__ A, const uint32_t* __restric
   lds_barrier();  // every wave is done with the ring
 
   if constexpr (KS > 1) {
-    // group g hands its accumulators to group 0 in round g (lane-major: word r * 64 + lane of
-    // the wave's slice); group 0 adds them in group order
-    float* pb = reinterpret_cast<float*>(As) + wv * (kWave * MI * NJ * 4);
-#pragma unroll 1
-    for (int g = 1; g < KS; ++g) {
-      if (ks == g) {
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-          for (int jj = 0; jj < NJ; ++jj)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) pb[((i * NJ + jj) * 4 + r) * kWave + lane] = acc[i][jj][r];
-      }
-      lds_barrier();
-      if (ks == 0) {
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-          for (int jj = 0; jj < NJ; ++jj)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[i][jj][r] += pb[((i * NJ + jj) * 4 + r) * kWave + lane];
-      }
-      lds_barrier();
-    }
+    k_group_handoff<KS>(acc, reinterpret_cast<float*>(As) + wv * (kWave * MI * NJ * 4), ks, lane);
     if (ks != 0) return;  // no barrier follows
   }
-
-  // epilogue: wave-private BM x 32 bf16 sub-tile at As + wv * BM * 32 (row stride 32), then
-  // 16-byte row segments; registers r, r + 1 are rows m, m + 1 of one column
-  uint16_t* lds = &As[wv * (BM * 32)];
-#pragma unroll
-  for (int i = 0; i < MI; ++i)
-#pragma unroll
-    for (int jj = 0; jj < NJ; ++jj)
-#pragma unroll
-      for (int r = 0; r < 4; r += 2) {
-        const int row = 16 * i + 4 * kg + r;
-        const uint32_t pk = pack_bf16x2_rne(acc[i][jj][r], acc[i][jj][r + 1]);
-        lds[row * 32 + 16 * jj + fr] = (uint16_t)pk;
-        lds[(row + 1) * 32 + 16 * jj + fr] = (uint16_t)(pk >> 16);
-      }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's sub-tile is in LDS
-  const int n0w = n0 + 32 * wv;
-  const int cr = lane >> 2, cc = lane & 3;
-  // whole 16-byte segments when the tile is inside C and C's rows are 16-byte aligned
-  const bool full = m0 + BM <= M && n0w + 32 <= N && (N & 7) == 0 &&
-                    (reinterpret_cast<uintptr_t>(C) & 15) == 0;
-#pragma unroll
-  for (int p = 0; p < BM / 16; ++p) {
-    const int row = 16 * p + cr;
-    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&lds[row * 32 + 8 * cc]);
-    const int m = m0 + row, n = n0w + 8 * cc;
-    if (full) {
-      *reinterpret_cast<u32x4_t*>(&C[(size_t)m * N + n]) = v;
-    } else if (m < M) {
-      for (int e = 0; e < 8; ++e)
-        if (n + e < N) C[(size_t)m * N + n + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
-    }
-  }
+  store_tile_16x16<BM>(acc, &As[wv * (BM * 32)], C, M, N, m0, n0 + 32 * wv, lane);
 }
 
 inline int ilog2(int g) { return 31 - __builtin_clz((unsigned)g); }
