@@ -328,6 +328,9 @@ def main():
         ms_eager = (time.perf_counter() - t0) * 1e3 / 10
         finite = bool(torch.isfinite(runner.logits).all())
         nbytes = shape.decode_bytes(ctx)
+        runner.graph = None
+        runner.cache_k = runner.cache_v = None
+        pre = prefill_pass(runner, shape)
         del runner
         torch.cuda.empty_cache()
         gbs = nbytes / (ms * 1e-3) / 1e9
@@ -335,7 +338,59 @@ def main():
                 "gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                 "bytes_per_token": nbytes, "hbm_floor_ms": round(nbytes / HBM_PEAK_GBS / 1e6, 4),
                 "eager_ms_per_token": round(ms_eager, 3), "context": ctx, "logits_finite": finite,
-                "timing": f"median of 5 x {reps} graph replays, hip events"}
+                "timing": f"median of 5 x {reps} graph replays, hip events"}, pre
+
+    def prefill_pass(runner, shape, tokens=(512, 2048), reps=3):
+        """The same model's prompt pass (Qwen2Runner.forward over T new tokens, last-token
+        logits): W4 GEMMs on the standard format (ns_w4_linear, ns_w4_linear_swiglu), then on the
+        packed tile format after pack_prefill (ns_w4_linear_packed, ns_w4_linear_packed_swiglu);
+        norms, rope and the causal attention as the runner runs them (attention in fp32
+        PyTorch). Median of reps passes after one warm pass, hip events."""
+        st = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+
+        def timed(ids):
+            runner.forward(ids, 0, last_only=True)
+            torch.cuda.synchronize()
+            ts = []
+            for _ in range(reps):
+                e0.record(st)
+                runner.forward(ids, 0, last_only=True)
+                e1.record(st)
+                torch.cuda.synchronize()
+                ts.append(e0.elapsed_time(e1))
+            return statistics.median(ts)
+
+        res = {}
+        for T in tokens:
+            ids = torch.randint(0, shape.vocab, (T,), generator=torch.Generator().manual_seed(9)).to(dev)
+            runner.packed = None
+            ms_std = timed(ids)
+            ref = runner.forward(ids, 0, last_only=True).float()
+            if runner.packed is None:
+                runner.pack_prefill()
+            ms_pk = timed(ids)
+            out = runner.forward(ids, 0, last_only=True).float()
+            gap = ((out - ref).abs().max() / ref.abs().max()).item()
+            cos = torch.nn.functional.cosine_similarity(out.flatten(), ref.flatten(), dim=0).item()
+            w4_flops = 2 * T * sum(n * kk for n, kk in (
+                (shape.qkv_rows, shape.hidden), (shape.hidden, shape.heads * shape.head_dim),
+                (2 * shape.intermediate, shape.hidden), (shape.hidden, shape.intermediate))) * shape.layers
+            res[f"t{T}"] = {"ms_standard": round(ms_std, 3), "ms_packed": round(ms_pk, 3),
+                            "tokens_per_s_standard": round(T / ms_std * 1e3, 1),
+                            "tokens_per_s_packed": round(T / ms_pk * 1e3, 1),
+                            "w4_tflops_packed": round(w4_flops / (ms_pk * 1e-3) / 1e12, 1),
+                            "logits_gap_packed_vs_standard": round(gap, 5),
+                            "logits_cos_packed_vs_standard": round(cos, 6)}
+        runner.packed = None
+        res["timing"] = (f"Qwen2.5-7B-shaped random-init runner, one prompt pass of T tokens from "
+                         f"position 0, median of {reps} after a warm pass, hip events; "
+                         "w4_tflops counts the W4 GEMM flops only (the pass also runs attention, "
+                         "norms, rope and the lm_head); the logits gap is max |packed - standard| / "
+                         "max |standard| of the last token: both formats stage the same bf16 weights "
+                         "and differ in fp32 summation order, which 28 random-init layers amplify")
+        return res
 
     def gptq_set():
         """The calibrated quantizer (ns_w4_gptq) on the gate_up and down layers: one call after a
@@ -482,7 +537,8 @@ def main():
         print(json.dumps({"packed_format": packed_sets()}), flush=True)
         return
     if args.decode_only:
-        print(json.dumps({"config5_decode": decode_step()}), flush=True)
+        dec, pre = decode_step()
+        print(json.dumps({"config5_decode": dec, "config5_prefill": pre}), flush=True)
         return
 
     def m8_set():
@@ -623,7 +679,7 @@ def main():
 
         extra["packed_format"] = packed_sets()
         extra["config4_gemm"] = gemm_set()
-        extra["config5_decode"] = decode_step()
+        extra["config5_decode"], extra["config5_prefill"] = decode_step()
         extra["gptq"] = gptq_set()
         extra["library_reference"] = library_reference()
 

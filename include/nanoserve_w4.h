@@ -113,6 +113,18 @@ int ns_w4_linear_packed(const void* X, const void* Wp, const void* Sp, void* Y, 
                         int K, int G, void* stream);
 
 /*
+ * No counterpart in the reference's C ABI: ns_w4_linear_packed's prefill GEMM followed by
+ * ns_swiglu (the reference MLP's swiglu(linear(h, "g"), linear(h, "u")), python/nanoserve/
+ * qwen.py:159) in one launch, on packed weights whose rows are gate and up rows interleaved in
+ * blocks of 8 as for ns_w4_linear_swiglu (N = 2 I, N % 16 == 0). Y [M][N/2] bf16 =
+ * bf16(silu(g) * u), g and u the bf16 outputs ns_w4_linear_packed gives for the gate and up
+ * rows, silu in fp32 as ns_swiglu. M > 16 only (batched decode keeps the GEMV and a separate
+ * SwiGLU). Returns -2 for M <= 16 and otherwise as ns_w4_linear_packed's GEMM.
+ */
+int ns_w4_linear_packed_swiglu(const void* X, const void* Wp, const void* Sp, void* Y, int M,
+                               int N, int K, int G, void* stream);
+
+/*
  * No counterpart in the reference's C ABI: ns_w4_linear followed by ns_swiglu, the reference's
  * MLP activation (python/nanoserve/qwen.py:159, swiglu(linear(h, "g"), linear(h, "u"))), in
  * one launch. The rows of Wq / S are gate and up rows interleaved in blocks of 8 (rows 16b ..

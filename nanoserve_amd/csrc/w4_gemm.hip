@@ -652,6 +652,48 @@ __device__ __forceinline__ void store_tile_16x16(const f32x4_t (&acc)[BM / 16][2
   }
 }
 
+// SwiGLU epilogue of the 16x16x32 GEMMs for gate/up weights interleaved in blocks of 8 rows
+// (features 16b .. 16b+7 gate, 16b+8 .. 16b+15 the matching up rows): lane (j, kg) holds feature
+// column j of its 16-column half, so a gate value (j < 8) finds its up value in lane j + 8 of the
+// same row. Y[m][o] = bf16(silu(g) * u) with g, u rounded to bf16 first (the values the plain
+// GEMM would store), o = 8 b + j; the wave's 16 outputs per row go through its private LDS
+// sub-tile (row stride 16) and out as 16-byte segments (element by element at the edges of Y or
+// when its rows are not 16-byte aligned).
+template <int BM>
+__device__ __forceinline__ void store_tile_16x16_swiglu(const f32x4_t (&acc)[BM / 16][2], uint16_t* lds,
+                                                        uint16_t* Y, int M, int N, int m0, int n0w,
+                                                        int lane) {
+  const int fr = lane & 15, kg = lane >> 4, Nh = N >> 1;
+#pragma unroll
+  for (int i = 0; i < BM / 16; ++i)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float g = round_bf16(acc[i][jj][r]);
+        const float u = lane_xor8(g);
+        if (fr < 8)
+          lds[(16 * i + 4 * kg + r) * 16 + 8 * jj + fr] = (uint16_t)f32_to_bf16_rne(silu_mul(g, u));
+      }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's sub-tile is in LDS
+  const int o0 = n0w >> 1;             // the wave's first output column
+  const bool full = m0 + BM <= M && n0w + 32 <= N && (Nh & 7) == 0 &&
+                    (reinterpret_cast<uintptr_t>(Y) & 15) == 0;
+  const int cr = lane >> 1, cc = lane & 1;
+#pragma unroll
+  for (int p = 0; p < BM / 32; ++p) {
+    const int row = 32 * p + cr;
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(&lds[row * 16 + 8 * cc]);
+    const int m = m0 + row, o = o0 + 8 * cc;
+    if (full) {
+      *reinterpret_cast<u32x4_t*>(&Y[(size_t)m * Nh + o]) = v;
+    } else if (m < M) {
+      for (int e = 0; e < 8; ++e)
+        if (2 * (o + e) < N) Y[(size_t)m * Nh + o + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+}
+
 // Packed tile format (ns_w4_repack: tiles of 16 rows x 128 k, lane l's 16 bytes = row l % 16 at
 // k = 32 s + 8 (l / 16) + e, word s, nibbles in the order e = 0 2 4 6 1 3 5 7) -> 8 staged weights
 // bf16_rne((q - 8) * s) in natural k order: with that nibble order the pairs (e0, e1), (e2, e3),
@@ -694,7 +736,7 @@ __device__ __forceinline__ u32x4_t dequant_word_bf16_pk(uint32_t w, uint32_t vma
 //    group per round, and group 0 adds them in group order.
 //  * Epilogue (group 0): each wave rounds its BM x 32 sub-tile to bf16 into a private part of
 //    the (then free) LDS ring and stores 16-byte row segments.
-template <int BM, int NWN, int KS, int WD>
+template <int BM, int NWN, int KS, int WD, bool SW = false>
 __global__ __launch_bounds__(NWN * KS * kWave, KS > 1 ? 1 : 4)
 void w4_gemm_pk_kernel(const uint16_t* __restrict__ A, const uint32_t* __restrict__ Wp,
                        const uint16_t* __restrict__ Sp, uint16_t* __restrict__ C, int M, int N, int K) {
@@ -843,7 +885,10 @@ void w4_gemm_pk_kernel(const uint16_t* __restrict__ A, const uint32_t* __restric
     k_group_handoff<KS>(acc, reinterpret_cast<float*>(As) + wv * (kWave * MI * NJ * 4), ks, lane);
     if (ks != 0) return;  // no barrier follows
   }
-  store_tile_16x16<BM>(acc, &As[wv * (BM * 32)], C, M, N, m0, n0 + 32 * wv, lane);
+  if constexpr (SW)
+    store_tile_16x16_swiglu<BM>(acc, &As[wv * (BM * 32)], C, M, N, m0, n0 + 32 * wv, lane);
+  else
+    store_tile_16x16<BM>(acc, &As[wv * (BM * 32)], C, M, N, m0, n0 + 32 * wv, lane);
 }
 
 inline int ilog2(int g) { return 31 - __builtin_clz((unsigned)g); }
@@ -951,24 +996,33 @@ int gemm_packed_plan(int M, int N, int K) {
   return 0;
 }
 
-hipError_t launch_gemm_packed(const uint16_t* A, const uint32_t* Wp, const uint16_t* Sp, uint16_t* C,
-                              int M, int N, int K, int plan, hipStream_t st) {
+namespace {
+template <bool SW>
+hipError_t launch_gemm_packed_t(const uint16_t* A, const uint32_t* Wp, const uint16_t* Sp, uint16_t* C,
+                                int M, int N, int K, int plan, hipStream_t st) {
   switch (plan) {
     case 0:  // 128 x 128 tiles
-      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 4, 1, 1>), dim3((N + 127) / 128, (M + 127) / 128),
+      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 4, 1, 1, SW>), dim3((N + 127) / 128, (M + 127) / 128),
                          dim3(256), 0, st, A, Wp, Sp, C, M, N, K);
       return hipSuccess;
     case 1:  // 128 x 128 tiles, K split over two groups of four waves
-      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 4, 2, 1>), dim3((N + 127) / 128, (M + 127) / 128),
+      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 4, 2, 1, SW>), dim3((N + 127) / 128, (M + 127) / 128),
                          dim3(512), 0, st, A, Wp, Sp, C, M, N, K);
       return hipSuccess;
     case 2:  // 128 x 64 tiles, K split over four groups of two waves
-      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 2, 4, 1>), dim3((N + 63) / 64, (M + 127) / 128),
+      hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 2, 4, 1, SW>), dim3((N + 63) / 64, (M + 127) / 128),
                          dim3(512), 0, st, A, Wp, Sp, C, M, N, K);
       return hipSuccess;
     default:
       return hipErrorInvalidValue;
   }
+}
+}  // namespace
+
+hipError_t launch_gemm_packed(const uint16_t* A, const uint32_t* Wp, const uint16_t* Sp, uint16_t* C,
+                              int M, int N, int K, int plan, bool swiglu, hipStream_t st) {
+  return swiglu ? launch_gemm_packed_t<true>(A, Wp, Sp, C, M, N, K, plan, st)
+                : launch_gemm_packed_t<false>(A, Wp, Sp, C, M, N, K, plan, st);
 }
 
 hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {

@@ -399,7 +399,7 @@ int ns_w4_linear_packed(const void* X, const void* Wp, const void* Sp, void* Y, 
   const auto y = static_cast<uint16_t*>(Y);
   hipError_t e;
   if (M > 16)
-    e = ns::launch_gemm_packed(x, wp, sp, y, M, N, K, ns::gemm_packed_plan(M, N, K), st);
+    e = ns::launch_gemm_packed(x, wp, sp, y, M, N, K, ns::gemm_packed_plan(M, N, K), false, st);
   else if (C <= 16)
     e = ns::launch_packed<16, 1>(x, wp, sp, y, M, N, K, st);
   else if (C <= 32)
@@ -408,6 +408,24 @@ int ns_w4_linear_packed(const void* X, const void* Wp, const void* Sp, void* Y, 
     e = ns::launch_packed_lds<16, 10>(x, wp, sp, y, M, N, K, st);
   else
     return -2;
+  if (e != hipSuccess) return static_cast<int>(e);
+  return static_cast<int>(hipGetLastError());
+}
+
+int ns_w4_linear_packed_swiglu(const void* X, const void* Wp, const void* Sp, void* Y, int M,
+                               int N, int K, int G, void* stream) {
+  // prefill only (M > 16): the GEMM on the packed tiles with the SwiGLU epilogue; the gate/up
+  // rows come interleaved in blocks of 8, so N is a multiple of 16
+  if (M <= 16 || N <= 0 || K <= 0 || G != 128 || K % 128 || N % 16) return -2;
+  if ((uint64_t)(M + 256) * (uint64_t)K * 2 >= (1ull << 31)) return -2;
+  if (ns::packed_weight_bytes(N, K) >= (1ull << 31)) return -2;
+  if (!X || !Wp || !Sp || !Y || !ns::aligned(X, 16) || !ns::aligned(Wp, 16) ||
+      !ns::aligned(Sp, 16) || !ns::aligned(Y, 2))
+    return -2;
+  const hipError_t e = ns::launch_gemm_packed(
+      static_cast<const uint16_t*>(X), static_cast<const uint32_t*>(Wp),
+      static_cast<const uint16_t*>(Sp), static_cast<uint16_t*>(Y), M, N, K,
+      ns::gemm_packed_plan(M, N, K), true, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return static_cast<int>(e);
   return static_cast<int>(hipGetLastError());
 }

@@ -39,6 +39,7 @@ SIGNATURES["ns_w4_gemv_decode"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _VP, _VP,
 SIGNATURES["ns_bf16_gemv"] = [_VP, _VP, _VP, _VP, _F32, _VP, _VP, _I32, _I32, _VP]
 SIGNATURES["ns_w4_repack"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_w4_linear_packed"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
+SIGNATURES["ns_w4_linear_packed_swiglu"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_w4_linear_swiglu"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP]
 SIGNATURES["ns_w4_linear_workspace"] = [_I32, _I32, _I32, _I32]
 SIGNATURES["ns_w4_linear_ws"] = [_VP, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _SZ, _VP]
@@ -503,6 +504,24 @@ class Kernels:
         rc = self.lib.ns_w4_linear_packed(x.contiguous().data_ptr(), Wp.data_ptr(), Sp.data_ptr(),
                                           out.data_ptr(), M, N, K, group, self._stream())
         self._check(rc, "ns_w4_linear_packed")
+        return out
+
+    def w4_linear_packed_swiglu(self, x, Wp, Sp, N, group=128, out=None):
+        """x [M, K] bf16 (M > 16) -> bf16(silu(g) * u) [M, N/2] on packed weights of gate/up
+        rows interleaved in blocks of 8 (qwen.interleave_gate_up, then w4_repack): the packed
+        GEMM with the SwiGLU epilogue (include/nanoserve_w4.h)."""
+        _require_gpu_tensor(x, "x", torch.bfloat16)
+        _require_gpu_tensor(Wp, "Wp", torch.int32)
+        _require_gpu_tensor(Sp, "Sp", torch.bfloat16)
+        M, K = x.shape
+        if Wp.shape[0] * 16 < N or Wp.shape[1] * 128 != K:
+            raise ValueError("packed weights do not match N and x's K")
+        if out is None:
+            out = torch.empty((M, N // 2), dtype=torch.bfloat16, device=x.device)
+        rc = self.lib.ns_w4_linear_packed_swiglu(x.contiguous().data_ptr(), Wp.data_ptr(),
+                                                 Sp.data_ptr(), out.data_ptr(), M, N, K, group,
+                                                 self._stream())
+        self._check(rc, "ns_w4_linear_packed_swiglu")
         return out
 
     # ------------------------------------------------------------------ measurement kernels

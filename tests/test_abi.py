@@ -35,6 +35,7 @@ def test_header_declares_the_reference_entry_points():
     # decode-step attention operators the reference does with PyTorch ops
     assert declared_symbols() == sorted([
         "ns_w4_linear", "ns_w4_quantize", "ns_w4_repack", "ns_w4_linear_packed",
+        "ns_w4_linear_packed_swiglu",
         "ns_rmsnorm", "ns_rope", "ns_swiglu",
         "ns_decode_qkv", "ns_decode_attention_workspace", "ns_decode_attention",
         "ns_decode_qkv_attention", "ns_w4_gemv_decode", "ns_w4_gemv_decode_attn", "ns_decode_embed",
@@ -305,6 +306,13 @@ def test_packed_entry_points_reject_bad_arguments(k):
     assert k.lib.ns_w4_linear_packed(P, P, P, P, 2, 64, 20608, 128, None) == -2  # K > 20480
     assert k.lib.ns_w4_linear_packed(P, P, P, P, 1, 64, 256, 128, None) == -2    # M = 1: ns_w4_linear
     assert k.lib.ns_w4_linear_packed(P + 8, P, P, P, 2, 64, 256, 128, None) == -2
+    # the SwiGLU GEMM: prefill only, gate/up rows in blocks of 8
+    assert k.lib.ns_w4_linear_packed_swiglu(P, P, P, P, 16, 64, 256, 128, None) == -2  # M <= 16
+    assert k.lib.ns_w4_linear_packed_swiglu(P, P, P, P, 32, 72, 256, 128, None) == -2  # N % 16
+    assert k.lib.ns_w4_linear_packed_swiglu(P, P, P, P, 32, 64, 200, 128, None) == -2  # K % 128
+    assert k.lib.ns_w4_linear_packed_swiglu(P, P, P, P, 32, 64, 256, 64, None) == -2   # G != 128
+    assert k.lib.ns_w4_linear_packed_swiglu(P, P, P, P, 17, 64, 3933184, 128, None) == -2
+    assert k.lib.ns_w4_linear_packed_swiglu(P, P + 8, P, P, 32, 64, 256, 128, None) == -2
 
 
 def test_gptq_workspace_and_rejects(k):

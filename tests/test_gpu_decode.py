@@ -559,6 +559,38 @@ def test_w4_linear_packed_gemm_graph_and_rows_past_tile(k):
 
 
 # ------------------------------------------------------------------ the runner
+@pytest.mark.parametrize("M,N,K", [(2048, 37888, 3584), (1024, 7168, 18944), (512, 3584, 3584),
+                                   (200, 1040, 1024), (17, 4096, 512), (300, 37888, 384)])
+def test_w4_linear_packed_swiglu(k, M, N, K):
+    """ns_w4_linear_packed_swiglu (the packed GEMM with the SwiGLU epilogue; on MI355X the first
+    shapes take the 128 x 128, two-group K-split and 128 x 64 plans, then ragged M and N) equals
+    ns_w4_linear_packed of the same interleaved weights followed by ns_swiglu of the
+    de-interleaved halves, bit for bit (the same accumulation; the products rounded to bf16
+    before the activation as the unfused pair stores them), and, where ns_w4_linear_swiglu takes
+    the shape, the standard format's fused GEMM to one bf16 rounding of its inputs."""
+    from nanoserve_amd.qwen import interleave_gate_up
+
+    print(f"w4_linear_packed_swiglu M={M} N={N} K={K}", flush=True)
+    Wq, S = interleave_gate_up(*_w4(N, K, seed=101))
+    Wp, Sp = k.w4_repack(Wq, S)
+    x = rnd(M, K, seed=102)
+    act = k.w4_linear_packed_swiglu(x, Wp, Sp, N)
+    I = N // 2
+    g4 = k.w4_linear_packed(x, Wp, Sp, N).view(M, I // 8, 2, 8)
+    ref = k.swiglu(g4[:, :, 0].reshape(M, I).contiguous(), g4[:, :, 1].reshape(M, I).contiguous())
+    torch.cuda.synchronize()
+    assert act.shape == (M, I)
+    assert torch.equal(act, ref)
+    if M % 128 == 0 and N % 128 == 0:
+        std = k.w4_linear_swiglu(x, Wq, S, 128)
+        torch.cuda.synchronize()
+        close(act, std.double().cpu(), rtol=2 ** -6, atol=1e-3 * std.abs().max().item())
+    out = torch.full((M + 3, I), 5.0, dtype=torch.bfloat16, device=DEV)
+    assert k.w4_linear_packed_swiglu(x, Wp, Sp, N, out=out[:M]) is not None
+    torch.cuda.synchronize()
+    assert torch.equal(out[:M], act) and (out[M:] == 5.0).all()
+
+
 def _hf_model(H, nh, nkv, I, V, layers, seed):
     pytest.importorskip("transformers")
     return R.tiny_qwen2(H, nh, nkv, I, V, layers, seed)
@@ -671,6 +703,39 @@ def test_runner_matches_hf_qwen2(k, H, nh, nkv, I, V, T, cache):
         out = runner.decode(ids[T + i].to(DEV), T + i).clone()
         torch.cuda.synchronize()
         assert torch.equal(out, eager[i]), i
+
+
+def test_runner_packed_prefill_matches_hf(k):
+    """Prompt passes on packed weights (pack_prefill: packed-format GEMMs for more than 16
+    tokens, the SwiGLU one for gate/up) match the HF model holding the runner's dequantized
+    weights, and the standard-format prompt pass to bf16 roundings; a 40-token prompt continued
+    by a 30-token chunk at position 40 (both packed) and decode steps after it read the cache
+    the packed passes wrote."""
+    V = 640
+    m = _hf_model(512, 4, 2, 768, V, layers=2, seed=2)
+    runner = Qwen2Runner.from_hf(m, device=DEV, kernels=k)
+    ref_model = _effective_hf(m, runner)
+    ids = torch.randint(0, V, (74,), generator=torch.Generator().manual_seed(3))
+    with torch.no_grad():
+        ref = ref_model(ids[None]).logits[0]
+    std = runner.forward(ids[:40].to(DEV), 0)
+    assert runner.pack_prefill() is runner
+    runner.alloc_cache(80)
+    first = runner.forward(ids[:40].to(DEV), 0, use_cache=True)
+    second = runner.forward(ids[40:70].to(DEV), 40, use_cache=True)
+    steps = [runner.forward(ids[70 + i:71 + i].to(DEV), 70 + i, use_cache=True) for i in range(4)]
+    torch.cuda.synchronize()
+    _check_logits(first, ref[:40])
+    _check_logits(second, ref[40:70])
+    for i in range(4):
+        _check_logits(steps[i], ref[70 + i:71 + i])
+    _check_logits(first, std.float().cpu())
+    # 16 tokens or fewer stay on the standard format
+    short = runner.forward(ids[:16].to(DEV), 0)
+    runner.packed = None
+    short_std = runner.forward(ids[:16].to(DEV), 0)
+    torch.cuda.synchronize()
+    assert torch.equal(short, short_std)
 
 
 def test_graph_replays_match_eager_with_work_between(k):
