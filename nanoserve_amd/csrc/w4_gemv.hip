@@ -1692,8 +1692,14 @@ struct M1Layout {
   bool xfirst = false;  // activation loads ahead of the workgroup's weight loads
 };
 
-// * Long rows (K / 128 >= 64, e.g. down): 16 waves per 16-row group; when the groups fit one
-//   per CU, each CU holds one workgroup and its activation goes first.
+// * Long rows (K / 128 >= 64, e.g. down): 16 waves, one workgroup per CU, activation first;
+//   16-row groups (persistent when there are more groups than CUs), or, when the 16-row groups
+//   would leave half the CUs or more idle, one round of ceil(N / CUs) rows per CU. On MI355X
+//   (interleaved A/B, us, same outputs bit for bit: every layout sums a row's partials in the
+//   same order): 8192 x 8192 9.19 -> 8.41 and 5120 x 27648 20.06 -> 19.46 against two
+//   workgroups per CU without the activation first; 1536 x 8960 6.08 -> 4.56 (6 rows per CU)
+//   and 2048 x 11008 6.28 -> 5.53 (8 rows) against 16-row groups on 96 and 128 CUs; the 7B down
+//   projection (224 groups) keeps 16-row groups (9.27 against 9.90 with 14 rows on every CU).
 // * Many groups (gate/up): the streaming plans, four seven-wave workgroups per CU when
 //   16 x 7 is a multiple of K / 128.
 // * Layers whose weights give every CU at most 32 blocks of 1 KiB (qkv, o): one workgroup per
@@ -1711,7 +1717,12 @@ hipError_t m1_layout(int N, int K, M1Layout* L) {
   M1Layout l;
   if (C >= 64) {
     l.nw = 16;
-    l.xfirst = groups16 <= cus;
+    l.wpc = 1;
+    l.xfirst = true;
+    if (2 * groups16 <= cus) {
+      l.gr = 0;
+      l.rows = (N + cus - 1) / cus;
+    }
   } else if (groups16 >= 1024 && C >= 14) {
     l.nw = 112 % C == 0 ? 7 : 14;
     l.wpc = l.nw == 7 ? 4 : 2;

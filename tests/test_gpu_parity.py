@@ -327,6 +327,20 @@ def test_gemv_m1_one_round_groups(kernels, oracle, N, K):
     check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
 
 
+@pytest.mark.parametrize("N,K", [(1536, 8960), (2048, 11008), (100, 8192), (8192, 8192),
+                                 (5120, 13824), (3584, 18944), (4100, 18944)])
+def test_gemv_m1_long_row_layouts(kernels, oracle, N, K):
+    """M = 1 with long rows (K / 128 >= 64) in each layout the planner picks on MI355X's 256
+    CUs: one round of ceil(N / CUs) rows per CU when 16-row groups would fill half the CUs or
+    fewer (6, 8 and 1 rows), 16-row groups one per CU (224 and 257 groups: the last group short),
+    and 16-row groups persistent over two rounds (512, 320 groups)."""
+    G = 128
+    Wq, S = synth.weights(N, K, G, seed=N + 5 * K)
+    X = synth.activations(1, K, seed=N + 13)
+    y = run_linear(kernels, X, Wq, S, G)
+    check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
+
+
 @pytest.mark.parametrize("M", [2, 5, 8])
 @pytest.mark.parametrize("N,K", [(24, 256), (200, 4096), (136, 4352), (72, 12288), (40, 16384),
                                  (24, 18944), (9, 20480)])
