@@ -75,6 +75,8 @@ def parse():
                         "under a profiler")
     p.add_argument("--decode-only", action="store_true",
                    help="only the config-5 decode step (28-layer W4 Qwen2.5-7B, context 1024)")
+    p.add_argument("--prefill-only", action="store_true",
+                   help="only the Qwen2.5-7B-shaped prompt pass on the standard and packed formats")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only 1 GiB device-to-device copies: the known-size reference for HBM "
                         "byte counters read under a profiler")
@@ -286,7 +288,7 @@ def main():
                 del xa
         return gemm
 
-    def decode_step(reps=40, ctx=1024):
+    def decode_step(reps=40, ctx=1024, decode=True, prefill=True):
         """config 5: one decode step of a random-init W4A16 Qwen2.5-7B (28 layers, fused QKV and
         gate+up, bf16 lm_head) at context 1024 with a bf16 KV cache filled with N(0,1); the step
         is one HIP graph replay: ns_decode_embed (embedding row + the position's rotation
@@ -298,6 +300,11 @@ def main():
 
         shape = Qwen2Shape()
         runner = Qwen2Runner.random(shape, device=dev, seed=7, kernels=kern)
+        if not decode:
+            pre = prefill_pass(runner, shape)
+            del runner
+            torch.cuda.empty_cache()
+            return None, pre
         runner.alloc_cache(ctx)
         gen = torch.Generator(device=dev).manual_seed(8)
         runner.cache_k.copy_(torch.randn(runner.cache_k.shape, generator=gen, device=dev))
@@ -330,7 +337,7 @@ def main():
         nbytes = shape.decode_bytes(ctx)
         runner.graph = None
         runner.cache_k = runner.cache_v = None
-        pre = prefill_pass(runner, shape)
+        pre = prefill_pass(runner, shape) if prefill else None
         del runner
         torch.cuda.empty_cache()
         gbs = nbytes / (ms * 1e-3) / 1e9
@@ -537,8 +544,12 @@ def main():
         print(json.dumps({"packed_format": packed_sets()}), flush=True)
         return
     if args.decode_only:
-        dec, pre = decode_step()
-        print(json.dumps({"config5_decode": dec, "config5_prefill": pre}), flush=True)
+        dec, _ = decode_step(prefill=False)
+        print(json.dumps({"config5_decode": dec}), flush=True)
+        return
+    if args.prefill_only:
+        _, pre = decode_step(decode=False)
+        print(json.dumps({"config5_prefill": pre}), flush=True)
         return
 
     def m8_set():
