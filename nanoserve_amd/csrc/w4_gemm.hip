@@ -373,15 +373,6 @@ __device__ __forceinline__ void wait_vmcnt_c() {
   __builtin_amdgcn_s_waitcnt(imm);
 }
 
-//
-// KS > 1 (tile grids too small to fill the chip, e.g. down at M = 512): KS groups of NWN waves
-// split K inside the workgroup. Group ks computes 64-k blocks ks, ks + KS, ... into its own
-// accumulators through its own part of the LDS ring (step t loads and computes block t KS + ks
-// in every group); at the end groups 1 .. KS-1 hand their accumulators to group 0 through LDS,
-// one group per round, and group 0 adds them in group order and stores the tile.
-// 256-row tiles carry 128 accumulators per lane: the launch bound asks for two waves per SIMD
-// (two four-wave workgroups per CU, or one eight-wave workgroup with KS = 2) so the compiler
-// keeps them in VGPRs beside the operands.
 // K-split handoff of the GEMMs: group g hands its accumulators (MI x NJ vectors of R floats) to
 // group 0 in round g through pb (this wave's slice of the free LDS ring, lane-major: word r * 64
 // + lane); group 0 adds them in group order. Every wave of the workgroup calls it (it holds
@@ -412,6 +403,14 @@ __device__ __forceinline__ void k_group_handoff(V (&acc)[MI][NJ], float* pb, int
   }
 }
 
+// KS > 1 (tile grids too small to fill the chip, e.g. down at M = 512): KS groups of NWN waves
+// split K inside the workgroup. Group ks computes 64-k blocks ks, ks + KS, ... into its own
+// accumulators through its own part of the LDS ring (step t loads and computes block t KS + ks
+// in every group); at the end groups 1 .. KS-1 hand their accumulators to group 0 through LDS,
+// one group per round, and group 0 adds them in group order and stores the tile.
+// 256-row tiles carry 128 accumulators per lane: the launch bound asks for two waves per SIMD
+// (two four-wave workgroups per CU, or one eight-wave workgroup with KS = 2) so the compiler
+// keeps them in VGPRs beside the operands.
 template <int BM, int WN, int NWN, int ST, bool SW = false, int KS = 1, int WD = 1>
 __global__ __launch_bounds__(NWN * KS * kWave, BM >= 256 && KS == 1 ? 2 : 1) void w4_gemm2_kernel(
     const uint16_t* __restrict__ A, const uint32_t* __restrict__ Wq,
@@ -903,7 +902,7 @@ constexpr TileCfg kCfgs[] = {
     {128, 256, 0.85f},  // 2: v1, BM 128, 4 waves x 64 cols
     {128, 128, 0.75f},  // 3: v1, BM 128, 4 waves x 32 cols
     {128, 128, 1.00f},  // 4: v2, BM 128, 4 waves x 32 cols, 3 stages
-    {64, 128, 1.00f},   // 5: v2, BM 64, 4 waves x 32 cols, K split over 2 wave groups, 4 stages
+    {128, 128, 1.00f},  // 5: v2, BM 128, K split over 2 wave groups of 4, 2 stages, two per CU
     {256, 128, 1.00f},  // 6: v2, BM 256, 4 waves x 32 cols, 2 stages, two workgroups per CU
     {256, 128, 1.00f},  // 7: v2, BM 256, K split over 2 wave groups of 4, 2 stages, one per CU
     {128, 64, 1.00f},   // 8: v2, BM 128, K split over 4 wave groups of 2, 2 stages, one per CU
@@ -936,21 +935,25 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
     //    quarters to all of the CUs once and K >= 8192: down 3584 x 18944 at M = 2048 320 -> 301
     //    and 303.6 -> 289.7 us on two boxes, 4096 x 14336 263 -> 244 us; with short K (3584 x
     //    3584: 68 -> 72) or 128 such tiles (half the CUs: 159 -> 206) 128 x 128 stays.
-    //  * When 128 x 128 tiles leave CUs idle, narrower tiles with K split four ways over wave
-    //    groups of two (each wave a 32-column slice): 128 x 64 tiles, one eight-wave workgroup per
-    //    CU, when they fill three quarters to all of the CUs (down at M = 512: 121.8 -> 102.2 us,
-    //    4096 x 14336 at M = 512 98.8 -> 86.2); else 64 x 64 tiles, two per CU, up to 2.25 rounds
-    //    (down at M = 256 113.6 -> 65.2 us, 3584 x 3584 24.7 -> 17.8, qkv at M = 512 40.0 -> 38.5;
-    //    128 x 64 tiles there: 94.4, 24.2 and, at 288 tiles, 47.0); else 64 x 128 tiles with K
-    //    split over two groups of four (the plan all of these replaced).
+    //  * When 128 x 128 tiles fill at most one round of the CUs, K split inside the workgroup:
+    //    128 x 64 tiles over four wave groups of two (each wave a 32-column slice), one eight-wave
+    //    workgroup per CU, when they fill three quarters to all of the CUs (down at M = 512:
+    //    121.8 -> 102.2 us, 4096 x 14336 at M = 512 98.8 -> 86.2); else, with more than half the
+    //    CUs holding a 128 x 128 tile, those tiles over two groups of four waves, two eight-wave
+    //    workgroups per CU (against the 64 x 64 plan below, us: 3584 x 18944 at M = 1024 219.1 ->
+    //    161.5, M = 768 210.3 -> 148.6, 3328 x 11008 at M = 1024 132.4 -> 93.9, qkv 4608 x 3584 at
+    //    M = 512 37.0 -> 32.6, 3584 x 3584 at M = 768 39.2 -> 32.7; at exactly one round, 4096 x
+    //    14336 at M = 1024, 144.5 -> 135.2 against 128 x 128 unsplit; where the 128 x 64 plan
+    //    applies it stays ahead: down at M = 512 95.3 against 146.4); else 64 x 64 tiles over
+    //    four groups of two, two per CU (down at M = 256 113.6 -> 65.2 us, 3584 x 3584 24.7 ->
+    //    17.8).
     const long tiles = (long)((M + 127) / 128) * ((N + 127) / 128);
     const long tiles256 = (long)((M + 255) / 256) * ((N + 127) / 128);
     const bool ks256 = tiles256 <= cus && 4 * tiles256 >= 3 * cus && K >= 8192;
     int c = ks256 ? 7 : tiles256 >= 4 * cus ? 6 : 4;
-    if (tiles < cus) {
+    if (tiles <= cus) {
       const long t128x64 = (long)((M + 127) / 128) * ((N + 63) / 64);
-      const long t64x64 = (long)((M + 63) / 64) * ((N + 63) / 64);
-      c = 4 * t128x64 >= 3 * cus && t128x64 <= cus ? 8 : 4 * t64x64 <= 9 * cus ? 9 : 5;
+      c = tiles < cus && 4 * t128x64 >= 3 * cus && t128x64 <= cus ? 8 : 2 * tiles > cus ? 5 : 9;
     }
     return GemmPlan{c, kCfgs[c].bm, kCfgs[c].bn};
   }
@@ -1045,8 +1048,8 @@ hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st) {
                          a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     case 5:
-      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4, false, 2>), grid, dim3(512), 0, st, a.A, a.Wq,
-                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      hipLaunchKernelGGL((w4_gemm2_kernel<128, 32, 4, 2, false, 2, kWeightAhead>), grid, dim3(512), 0, st, a.A,
+                         a.Wq, a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     case 6:
       hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2, false, 1, kWeightAhead>), grid, dim3(256), 0, st, a.A, a.Wq, a.S,
@@ -1077,8 +1080,8 @@ hipError_t launch_gemm_swiglu(const GemmArgs& a, const GemmPlan& p, hipStream_t 
                          a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     case 5:
-      hipLaunchKernelGGL((w4_gemm2_kernel<64, 32, 4, 4, true, 2>), grid, dim3(512), 0, st, a.A, a.Wq,
-                         a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
+      hipLaunchKernelGGL((w4_gemm2_kernel<128, 32, 4, 2, true, 2, kWeightAhead>), grid, dim3(512), 0, st, a.A,
+                         a.Wq, a.S, a.C, a.M, a.N, a.K, ilog2(a.G));
       return hipSuccess;
     case 6:
       hipLaunchKernelGGL((w4_gemm2_kernel<256, 32, 4, 2, true, 1, kWeightAhead>), grid, dim3(256), 0, st, a.A, a.Wq,

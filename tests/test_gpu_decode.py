@@ -369,7 +369,7 @@ def test_gemv_decode_swiglu_output(k, N, K, norm):
 @pytest.mark.parametrize("M,N,K,G", [(128, 256, 256, 128), (256, 2048, 1024, 64),
                                      (2048, 37888, 3584, 128), (128, 7168, 18944, 128),
                                      (2048, 3584, 8192, 128), (512, 3584, 8192, 128),
-                                     (256, 3584, 3584, 128),
+                                     (256, 3584, 3584, 128), (768, 4608, 3584, 128),
                                      (384, 512, 512, 32), (1, 37888, 3584, 128),
                                      (3, 1024, 512, 128), (200, 1024, 512, 128)])
 def test_linear_swiglu_equals_linear_then_swiglu(k, M, N, K, G):

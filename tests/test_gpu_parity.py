@@ -438,14 +438,15 @@ def test_gemm_configs_sampled_rows(kernels, oracle, name, N, K, M):
 
 @pytest.mark.parametrize("M,N,K", [(1536, 4224, 8192), (2048, 4096, 14336), (512, 4096, 14336),
                                    (256, 3584, 18944), (256, 3584, 3584), (128, 7168, 3584),
-                                   (512, 7936, 1024)])
+                                   (512, 7936, 1024), (1024, 3584, 18944), (768, 4608, 3584),
+                                   (1024, 4096, 14336)])
 def test_gemm_ksplit_plans(kernels, oracle, M, N, K):
-    """The plans that split K inside the workgroup, on shapes besides the config-4 ones: 256 x 128
-    tiles over two wave groups (198 tiles, fewer than the CUs, at the shortest K the plan takes;
-    256 tiles of a Llama-3-8B down projection), 128 x 64 tiles over four groups (256 tiles) and
-    64 x 64 tiles over four groups (224 tiles at long and short K, 224 with N = 7168), and 64 x 128
-    tiles over two groups of four where the 64 x 64 grid would need more than 2.25 rounds
-    (248 128 x 128 tiles, 992 64 x 64 tiles)."""
+    """The plans that split K inside the workgroup, on shapes besides the config-4 ones (tile
+    counts for MI355X's 256 CUs): 256 x 128 tiles over two wave groups (198 tiles, fewer than the
+    CUs, at the shortest K the plan takes; 256 tiles of a Llama-3-8B down projection), 128 x 64
+    tiles over four groups (256 tiles), 64 x 64 tiles over four groups (224 tiles at long and
+    short K, 224 with N = 7168), and 128 x 128 tiles over two groups of four where those fill more
+    than half the CUs (248 tiles at K = 1024, 224 at K = 18944, 216, and exactly one round, 256)."""
     print(f"gemm ksplit M={M} N={N} K={K}", flush=True)
     _gemm_full_check(kernels, oracle, M, N, K, 128, seed=M + N)
 
