@@ -980,23 +980,33 @@ GemmPlan gemm_plan(int M, int N, int K, int G) {
 constexpr int kWeightAhead = 3;
 
 // Tile plan of the packed-format GEMM (M > 16 through ns_w4_linear_packed). On MI355X (interleaved
-// A/B runs on the config-4 shapes, us; the standard GEMM in brackets): 128 x 128 tiles, four
-// workgroups per CU, by default (gate/up 37888 x 3584 at M = 512 133.0 [152.2], at M = 2048 476.3
-// [530.8]); the same tiles with K split over two wave groups (one eight-wave workgroup per CU)
-// when K >= 8192 and the tiles make at most two rounds of the CUs (down 3584 x 18944 at M = 2048:
-// 266.2 [298.2], 300.5 unsplit, 284.4 for 256 x 128 tiles split the same way); 128 x 64 tiles
-// with K split over four groups of two waves when 128 x 128 tiles would leave CUs idle and the
-// 128 x 64 ones fill three quarters to all of them (down at M = 512: 98.8 [102.3], 189.8 for
-// 128 x 128 tiles). Weights one tile column (128 k) ahead in every plan: two columns ahead ran
-// 3-8 % slower (gate/up at M = 2048 489.6 against 473.0, M = 512 142.9 against 132.4), three 13 %.
+// A/B runs, us; the standard GEMM in brackets where the shape is a config-4 one):
+//  * 128 x 128 tiles, four workgroups per CU, when they make more than two rounds of the CUs
+//    (gate/up 37888 x 3584 at M = 512 133.0 [152.2], at M = 2048 476.3 [530.8]; qkv 4608 x 3584
+//    at M = 2048 77.4 against 81.3 split).
+//  * The same tiles with K split over two wave groups (one eight-wave workgroup, two per CU)
+//    when they make one to two rounds (down 3584 x 18944 at M = 2048: 266.2 [298.2], 300.5
+//    unsplit, 284.4 for 256 x 128 tiles split the same way; at short K too: qkv at M = 512 31.8
+//    against 39.4 unsplit, at M = 1024 49.6 against 54.1, 3584 x 3584 at M = 2048 57.0 against
+//    62.7, gate/up at M = 128 50.3 against 54.4).
+//  * 128 x 64 tiles with K split over four groups of two waves when 128 x 128 tiles would leave
+//    CUs idle and the 128 x 64 ones fill three quarters to all of them (down at M = 512: 98.8
+//    [102.3], 189.8 for 128 x 128 tiles; 3584 x 3584 at M = 512 24.1 against 31.4 split in two).
+//  * 64 x 64 tiles with K split over four groups of two waves, two per CU, on smaller grids
+//    (down at M = 256 57.7 against 89.3 for 128 x 64 tiles and 140.5 for the two-group split,
+//    64.6 for the standard GEMM; 3584 x 3584 at M = 256 15.4 against 22.4; qkv at M = 128 15.1
+//    against 22.4).
+// Weights one tile column (128 k) ahead in every plan: two columns ahead ran 3-8 % slower
+// (gate/up at M = 2048 489.6 against 473.0, M = 512 142.9 against 132.4), three 13 %.
 int gemm_packed_plan(int M, int N, int K) {
+  (void)K;
   int cus = 256;  // the device's CU count (a failed query leaves MI355X's; the launch reports it)
   if (cached_cu_count(&cus) != hipSuccess || cus <= 0) cus = 256;
   const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
   const long t128x64 = (long)((M + 127) / 128) * ((N + 63) / 64);
   if (t128 < cus && 4 * t128x64 >= 3 * cus && t128x64 <= cus) return 2;
-  if (K >= 8192 && t128 <= 2 * cus) return 1;
-  return 0;
+  if (t128 > 2 * cus) return 0;
+  return 2 * t128 > cus ? 1 : 3;
 }
 
 namespace {
@@ -1014,6 +1024,10 @@ hipError_t launch_gemm_packed_t(const uint16_t* A, const uint32_t* Wp, const uin
       return hipSuccess;
     case 2:  // 128 x 64 tiles, K split over four groups of two waves
       hipLaunchKernelGGL((w4_gemm_pk_kernel<128, 2, 4, 1, SW>), dim3((N + 63) / 64, (M + 127) / 128),
+                         dim3(512), 0, st, A, Wp, Sp, C, M, N, K);
+      return hipSuccess;
+    case 3:  // 64 x 64 tiles, K split over four groups of two waves
+      hipLaunchKernelGGL((w4_gemm_pk_kernel<64, 2, 4, 1, SW>), dim3((N + 63) / 64, (M + 63) / 64),
                          dim3(512), 0, st, A, Wp, Sp, C, M, N, K);
       return hipSuccess;
     default:

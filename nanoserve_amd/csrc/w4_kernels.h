@@ -98,7 +98,8 @@ GemmPlan gemm_plan(int M, int N, int K, int G);
 hipError_t launch_gemm(const GemmArgs& a, const GemmPlan& p, hipStream_t st);
 // GEMM on the packed tile format (ns_w4_repack's Wp, Sp), K % 128 == 0, any M >= 1; plan from
 // gemm_packed_plan (0: 128 x 128 tiles, 1: the same with K split over two wave groups,
-// 2: 128 x 64 tiles with K split over four). swiglu: rows are gate/up interleaved in blocks of 8
+// 2: 128 x 64 tiles with K split over four, 3: 64 x 64 tiles with K split over four). swiglu:
+// rows are gate/up interleaved in blocks of 8
 // (N % 16 == 0) and C [M][N/2] receives bf16(silu(g) * u).
 int gemm_packed_plan(int M, int N, int K);
 hipError_t launch_gemm_packed(const uint16_t* A, const uint32_t* Wp, const uint16_t* Sp, uint16_t* C,
