@@ -995,13 +995,15 @@ constexpr int kWeightAhead = 3;
 //  * 64 x 64 tiles with K split over four groups of two waves, two per CU, on smaller grids
 //    (down at M = 256 57.7 against 89.3 for 128 x 64 tiles and 140.5 for the two-group split,
 //    64.6 for the standard GEMM; 3584 x 3584 at M = 256 15.4 against 22.4; qkv at M = 128 15.1
-//    against 22.4).
+//    against 22.4) and whenever M <= 64, where 128-row tiles would be half empty (gate/up at
+//    M = 32 33.7 against 49.7 for the two-group split).
 // Weights one tile column (128 k) ahead in every plan: two columns ahead ran 3-8 % slower
 // (gate/up at M = 2048 489.6 against 473.0, M = 512 142.9 against 132.4), three 13 %.
 int gemm_packed_plan(int M, int N, int K) {
   (void)K;
   int cus = 256;  // the device's CU count (a failed query leaves MI355X's; the launch reports it)
   if (cached_cu_count(&cus) != hipSuccess || cus <= 0) cus = 256;
+  if (M <= 64) return 3;
   const long t128 = (long)((M + 127) / 128) * ((N + 127) / 128);
   const long t128x64 = (long)((M + 127) / 128) * ((N + 63) / 64);
   if (t128 < cus && 4 * t128x64 >= 3 * cus && t128x64 <= cus) return 2;

@@ -481,7 +481,8 @@ def test_w4_linear_packed_equals_w4_linear(k, N, K, M):
 
 
 @pytest.mark.parametrize("M,N,K", [(17, 200, 1024), (129, 1000, 3584), (300, 264, 8448), (64, 40, 384),
-                                   (33, 4608, 3584), (256, 3584, 18944), (512, 4608, 3584)])
+                                   (33, 4608, 3584), (256, 3584, 18944), (512, 4608, 3584),
+                                   (40, 20000, 384)])
 def test_w4_linear_packed_gemm(k, M, N, K):
     """M > 16 on packed weights runs the prefill GEMM on the packed tiles, with the reference
     GEMM's numerics: within half a bf16 ulp (+1e-5 ||ref||) of the oracle's product with every
@@ -560,7 +561,8 @@ def test_w4_linear_packed_gemm_graph_and_rows_past_tile(k):
 
 # ------------------------------------------------------------------ the runner
 @pytest.mark.parametrize("M,N,K", [(2048, 37888, 3584), (1024, 7168, 18944), (512, 3584, 3584),
-                                   (200, 1040, 1024), (17, 4096, 512), (300, 37888, 384)])
+                                   (200, 1040, 1024), (17, 4096, 512), (300, 37888, 384),
+                                   (40, 37888, 384)])
 def test_w4_linear_packed_swiglu(k, M, N, K):
     """ns_w4_linear_packed_swiglu (the packed GEMM with the SwiGLU epilogue; on MI355X the first
     shapes take the 128 x 128, two-group K-split and 128 x 64 plans, then ragged M and N) equals
