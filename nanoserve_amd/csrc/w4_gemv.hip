@@ -1639,6 +1639,13 @@ hipError_t launch_m8_auto(const GemvArgs& a, int nw, const M8Split& sp, hipStrea
   if (e != hipSuccess) return e;
   const double xb = 2.0 * a.M * a.K / sp.ks, rowb = 0.5 * a.K / sp.ks;
   const int ntiles = (a.N + 7) / 8;
+  // Two refinements of the byte count, measured on MI355X (M = 8 / M = 4, us): with one pair
+  // per wave and twelve or more waves, 32-row groups whenever they fill every CU (fewer group
+  // barriers: 28672 x 4096 17.8 / 17.2 -> 16.6 / 16.0; the 7B gate/up already took them); with
+  // six waves or fewer, two workgroups per CU at least (17920 x 1536 8.3 / 8.0 -> 6.5 / 6.1).
+  if (CW == 1 && sp.ks == 1 && nw >= 12 && (ntiles + 3) / 4 >= cus && pc4 >= 1)
+    return launch_m8<CW, 4, 4>(a, nw, 1, sp, st);
+  const int min_cap = sp.ks == 1 && nw <= 6 ? 2 : 1;
   struct Cand {
     int gt, cap, wgs;
     double cost;
@@ -1646,7 +1653,7 @@ hipError_t launch_m8_auto(const GemvArgs& a, int nw, const M8Split& sp, hipStrea
   int nc = 0;
   double best = 0;
   for (int gt = 4; gt >= 2; gt -= 2) {
-    for (int cap = 1; cap <= min(2, gt == 4 ? pc4 : pc2); ++cap) {
+    for (int cap = min(min_cap, gt == 4 ? pc4 : pc2); cap <= min(2, gt == 4 ? pc4 : pc2); ++cap) {
       const int groups = (ntiles + gt - 1) / gt;
       const int wgs = max(1, min(groups, cap * cus / sp.ks));
       const int gpw = (groups + wgs - 1) / wgs, wpc = (sp.ks * wgs + cus - 1) / cus;

@@ -341,6 +341,18 @@ def test_gemv_m1_long_row_layouts(kernels, oracle, N, K):
     check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
 
 
+@pytest.mark.parametrize("M,N,K", [(8, 17920, 1536), (2, 17920, 1536), (4, 28672, 4096), (7, 28672, 4096)])
+def test_gemv_small_batch_wide_layers(kernels, oracle, M, N, K):
+    """M = 2..8 layouts the group planner picks for wide layers beyond the 7B set (on MI355X's 256
+    CUs): two workgroups per CU at six waves (1.5B gate/up, 6 pairs), 32-row groups at sixteen
+    waves when they fill every CU (Llama-3-8B gate/up, 16 pairs)."""
+    G = 128
+    Wq, S = synth.weights(N, K, G, seed=N + K + M)
+    X = synth.activations(M, K, seed=M + 21, per_row_seed=True)
+    y = run_linear(kernels, X, Wq, S, G)
+    check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
+
+
 @pytest.mark.parametrize("M", [2, 5, 8])
 @pytest.mark.parametrize("N,K", [(24, 256), (200, 4096), (136, 4352), (72, 12288), (40, 16384),
                                  (24, 18944), (9, 20480)])
