@@ -1699,21 +1699,33 @@ struct M1Layout {
   bool xfirst = false;  // activation loads ahead of the workgroup's weight loads
 };
 
-// * Long rows (K / 128 >= 64, e.g. down): 16 waves, one workgroup per CU, activation first;
-//   16-row groups (persistent when there are more groups than CUs), or, when the 16-row groups
-//   would leave half the CUs or more idle, one round of ceil(N / CUs) rows per CU. On MI355X
-//   (interleaved A/B, us, same outputs bit for bit: every layout sums a row's partials in the
-//   same order): 8192 x 8192 9.19 -> 8.41 and 5120 x 27648 20.06 -> 19.46 against two
-//   workgroups per CU without the activation first; 1536 x 8960 6.08 -> 4.56 (6 rows per CU)
-//   and 2048 x 11008 6.28 -> 5.53 (8 rows) against 16-row groups on 96 and 128 CUs; the 7B down
-//   projection (224 groups) keeps 16-row groups (9.27 against 9.90 with 14 rows on every CU).
-// * Many groups (gate/up): the streaming plans, four seven-wave workgroups per CU when
-//   16 x 7 is a multiple of K / 128.
-// * Layers whose weights give every CU at most 32 blocks of 1 KiB (qkv, o): one workgroup per
-//   CU with ceil(N / CUs) rows, all of its blocks in flight at once (two per wave), activation
-//   first. On MI355X: qkv 5.40 -> 4.96 us, o 5.19 -> 4.59 us against the 8-row / 16-row
-//   groups at two workgroups per CU; down 10.73 -> 10.07 us with its activation first (one
-//   interleaved run, same outputs).
+// Layouts by shape (C = K / 128 k-groups, so a 16-row group is C blocks of 1 KiB). A wave count
+// NW "fits" C when C % NW == 0 (every wave streams the same number of a group's blocks) and
+// 16 NW % C == 0 (FC: each lane meets one k-group, its activation fragments stay in registers).
+// All layouts sum a row's partials in one of two fixed orders, and a shape's plain and fused
+// entry points take the same layout, so they give the same bits. Measured on MI355X (256 CUs,
+// interleaved A/B runs, us; 7B shapes first, then other model shapes the planner was checked on):
+// * Long rows (C >= 64, e.g. down): one workgroup per CU, activation first. Sixteen waves over
+//   16-row groups when those fill between half and all of the CUs once (the 7B down, 224
+//   groups: 8.83, against 9.57 with 14 rows on every CU) or make two or more full rounds
+//   (8192 x 8192, 512 groups: 8.36 against 9.44 in one round of 32 rows); otherwise one round
+//   of ceil(N / CUs) rows per CU: sixteen waves when the groups would fill half the CUs or fewer
+//   (1536 x 8960 6.06 -> 4.56 with 6 rows per CU, 2048 x 11008 6.22 -> 5.48), fourteen when
+//   they make one to two rounds (5120 x 13824, 320 groups: 12.34 -> 9.28; sixteen waves 9.66)
+//   or when fourteen gives FC (C = 112: 4096 x 14336 8.26 -> 8.06; C = 224: 8192 x 28672 22.6
+//   either way).
+// * Many groups (gate/up: at least 1024 16-row groups, C >= 14): 16-row groups, four seven-wave
+//   workgroups per CU where seven waves fit C (the 7B gate/up, C = 28: 13.7 against 15.6 with
+//   eight waves), two eight-wave ones where C % 8 == 0 (22016 x 2048 8.00 -> 6.83 and 28672 x
+//   4096 13.55 -> 12.11 against one round per CU), else fourteen waves, two per CU.
+// * Tiny layers (at most 10 blocks per CU in one round): 16-row groups of eight waves, two per
+//   CU (2048 x 1536 4.17 -> 3.49, 2048 x 2048 4.19 -> 3.46 against one round per CU).
+// * Layers of at most 32 blocks per CU in one round (qkv, o), or 80 with fewer than 512 16-row
+//   groups: one workgroup per CU with ceil(N / CUs) rows, activation first; fourteen waves past
+//   32 blocks or where 14 fits C up to 28 blocks, else sixteen (qkv 5.71 -> 4.68, o 4.68 -> 4.41
+//   against 16-row groups at eight waves, two per CU; 5120 x 5120 6.92 -> 5.54 and 6144 x 4096
+//   5.92 -> 5.47 likewise; with 1120 groups, 17920 x 1536, 16-row groups stay ahead: 5.99
+//   against 6.52 in one round).
 // * Otherwise eight waves per 16-row group (8-row groups when 16-row ones would give each CU
 //   only one or two), two workgroups per CU.
 hipError_t m1_layout(int N, int K, M1Layout* L) {
@@ -1721,23 +1733,27 @@ hipError_t m1_layout(int N, int K, M1Layout* L) {
   const hipError_t e = cached_cu_count(&cus);
   if (e != hipSuccess) return e;
   const int C = K >> 7, groups16 = (N + 15) / 16;
+  const int rows1 = (N + cus - 1) / cus, blocks1 = (rows1 * C + 15) / 16;
   M1Layout l;
   if (C >= 64) {
+    const bool fc14 = (16 * 14) % C == 0;
     l.nw = 16;
     l.wpc = 1;
     l.xfirst = true;
-    if (2 * groups16 <= cus) {
-      l.gr = 0;
-      l.rows = (N + cus - 1) / cus;
+    if (groups16 <= 2 * cus && (fc14 || 2 * groups16 <= cus || (groups16 > cus && groups16 < 2 * cus))) {
+      l.gr = 0;  // one round of ceil(N / CUs) rows per CU
+      l.rows = rows1;
+      if (fc14 || groups16 > cus) l.nw = 14;
     }
   } else if (groups16 >= 1024 && C >= 14) {
-    l.nw = 112 % C == 0 ? 7 : 14;
+    l.nw = C % 7 == 0 && 112 % C == 0 ? 7 : C % 8 == 0 ? 8 : 14;
     l.wpc = l.nw == 7 ? 4 : 2;
-  } else if (const int rows = (N + cus - 1) / cus; (rows * C + 15) / 16 <= 32) {
-    const int blocks = (rows * C + 15) / 16;
-    l.nw = 224 % C == 0 && blocks <= 28 ? 14 : 16;
+  } else if (blocks1 <= 10) {
+    l.nw = 8;
+  } else if (blocks1 <= 32 || (blocks1 <= 80 && groups16 < 512)) {
+    l.nw = blocks1 > 32 || (blocks1 <= 28 && 224 % C == 0) ? 14 : 16;
     l.gr = 0;
-    l.rows = rows;
+    l.rows = rows1;
     l.wpc = 1;
     l.xfirst = true;
   } else {
@@ -1848,11 +1864,13 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st, flo
     // 14.7 -> 14.2 us on MI355X against fourteen-wave workgroups, two per CU; same outputs)
     if (L.nw == 7) return launch_m1<7, 2, 16>(a, st, fz, L.wpc);
     if (L.nw == 14) return launch_m1<14, 2, 16>(a, st, fz, L.wpc);
-    // Eight-wave plans run with seven waves when 16 x 7 is a multiple of K / 128: each lane
-    // then meets one k-group only and keeps its activation fragments in registers (same
-    // outputs). The fused decode entries keep eight waves (their activation staging needs one
-    // vector per thread).
-    const bool fc7 = 112 % (a.K >> 7) == 0;
+    // Eight-wave plans run with seven waves when seven fits K / 128 (C % 7 == 0 and 16 x 7 a
+    // multiple of C): each lane then meets one k-group only and keeps its activation fragments
+    // in registers (same outputs). Without C % 7 == 0 the seven waves stream unequal shares
+    // (C = 16: 22016 x 2048 9.70 against 6.91 us with eight waves on MI355X). The fused decode
+    // entries keep eight waves (their activation staging needs one vector per thread).
+    const int C = a.K >> 7;
+    const bool fc7 = C % 7 == 0 && 112 % C == 0;
     if (L.gr == 16) return fc7 ? launch_m1<7, 2, 16>(a, st, fz, L.wpc) : launch_m1<8, 2, 16>(a, st, fz, L.wpc);
     return fc7 ? launch_m1<7, 2, 8>(a, st, fz, L.wpc) : launch_m1<8, 2, 8>(a, st, fz, L.wpc);
   }

@@ -283,6 +283,30 @@ def test_gemv_decode_attn_merges_splits(k, max_len):
             close(y, ref.double().cpu(), rtol=2 ** -6, atol=2e-3 * ref.abs().max().item())
 
 
+@pytest.mark.parametrize("Hq,Hk,N", [(12, 2, 1536), (16, 2, 2048), (32, 8, 4096), (40, 8, 5120),
+                                     (64, 8, 8192)])
+def test_gemv_decode_attn_model_shapes(k, Hq, Hk, N):
+    """The attention-merging o GEMV at the head counts and widths of other model sizes (1.5B,
+    3B, Llama-3-8B, 14B/32B, 72B): each takes a layout of the plain GEMV's planner with room
+    for the merged activation, and one split gives the plain GEMV's bits."""
+    D, max_len, pos = 128, 256, 50
+    qn, kn = Hq * D, Hk * D
+    Wq, S = _w4(N, qn, seed=Hq + N)
+    freq = R.inv_freq(D, 1000000.0).to(DEV)
+    work_a = k.decode_attention_workspace(Hq, Hk, D, max_len)
+    work_b = k.decode_attention_workspace(Hq, Hk, D, max_len)
+    kc, vc = rnd(Hk, max_len, D, seed=Hq + 1), rnd(Hk, max_len, D, seed=Hq + 2)
+    qkv = rnd(qn + 2 * kn, seed=Hq + 3, scale=0.5)
+    p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+    merged = k.decode_qkv_attention(qkv, None, freq, p, kc, vc, Hq, Hk, D, work_a)
+    ref = k.w4_linear(merged, Wq, S, 128)
+    a = torch.empty_like(merged)
+    k.decode_qkv_attention(qkv, None, freq, p, kc, vc, Hq, Hk, D, work_b, out=a, merge=False)
+    y = k.gemv_decode_attn(a, work_b, p, max_len, Hq, Wq, S)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref)
+
+
 # ------------------------------------------------------------------ ns_w4_gemv_decode
 def _w4(N, K, seed):
     """Quantized random weights (GPU), as the runner's: N(0, 0.02) bf16 through the quantizer."""

@@ -341,6 +341,23 @@ def test_gemv_m1_long_row_layouts(kernels, oracle, N, K):
     check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
 
 
+@pytest.mark.parametrize("N,K", [(2048, 1536), (2560, 2048), (22016, 2048), (17920, 1536),
+                                 (8960, 1536), (6144, 4096), (28672, 4096), (5120, 5120),
+                                 (4096, 14336)])
+def test_gemv_m1_model_layouts(kernels, oracle, N, K):
+    """M = 1 layouts the planner picks for layers of other model sizes (on MI355X's 256 CUs):
+    eight-wave 16-row groups, two per CU, for tiny layers and for wide ones whose K / 128 is a
+    multiple of 8 but not of 7 (2048 x 1536, 2560 x 2048, 22016 x 2048, 28672 x 4096), 16-row
+    groups past 512 groups with short rows (17920 x 1536), one round per CU at sixteen or fourteen
+    waves (8960 x 1536, 6144 x 4096, 5120 x 5120) and fourteen waves where they fit
+    K / 128 = 112 (4096 x 14336)."""
+    G = 128
+    Wq, S = synth.weights(N, K, G, seed=N + 7 * K)
+    X = synth.activations(1, K, seed=N + 17)
+    y = run_linear(kernels, X, Wq, S, G)
+    check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
+
+
 @pytest.mark.parametrize("M,N,K", [(8, 17920, 1536), (2, 17920, 1536), (4, 28672, 4096), (7, 28672, 4096)])
 def test_gemv_small_batch_wide_layers(kernels, oracle, M, N, K):
     """M = 2..8 layouts the group planner picks for wide layers beyond the 7B set (on MI355X's 256
