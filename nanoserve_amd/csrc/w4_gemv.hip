@@ -1522,7 +1522,9 @@ hipError_t launch_xlds(const GemvArgs& a, hipStream_t st) {
 template <int NW, int R, int GR, int XM, int YM, int XV, bool FC, bool XF>
 hipError_t launch_m1_fc(const GemvArgs& a, hipStream_t st, const M1Fuse& fz, int wpc) {
   const void* fn = reinterpret_cast<const void*>(&w4_gemv_m1_kernel<NW, R, GR, XM, YM, XV, FC, XF>);
-  // the planner keeps the dynamic part under 96 KiB; the limit leaves room for static LDS
+  // the dynamic part stays under this limit: 96 KiB at 16-row groups (the M = 1 filter), at most
+  // 127 KiB for one round of up to 32 long rows per CU; the rest of the CU's 160 KiB holds the
+  // static LDS
   const hipError_t attr = cached_max_dynamic_lds(fn, 128 * 1024);
   if (attr != hipSuccess) return attr;
   const int rows = GR > 0 ? GR : fz.rows;

@@ -315,11 +315,13 @@ def test_gemv_m1_kgroup_counts(kernels, oracle, N, K):
 
 
 @pytest.mark.parametrize("N,K", [(4608, 3584), (3584, 3584), (4100, 3584), (4609, 3584), (257, 2560),
-                                 (5000, 1024), (8960, 1536), (255, 256)])
+                                 (5000, 1024), (8960, 1536), (255, 256), (16384, 512), (12288, 1024),
+                                 (20480, 768)])
 def test_gemv_m1_one_round_groups(kernels, oracle, N, K):
     """M = 1 shapes small enough for one workgroup per CU with ceil(N / CUs) rows each: row
     groups whose pieces end inside a 1 KiB block (the last block partly another group's), a last
-    group shorter than the rest (N tails), and (4609, 3584) just past the one-round limit."""
+    group shorter than the rest (N tails), (4609, 3584) just past the one-round limit, and short
+    rows with more rows per CU than waves (64, 48 and 80 rows on 14, 14 and 16 waves)."""
     G = 128
     Wq, S = synth.weights(N, K, G, seed=N * 3 + K)
     X = synth.activations(1, K, seed=N + 11)
@@ -328,12 +330,13 @@ def test_gemv_m1_one_round_groups(kernels, oracle, N, K):
 
 
 @pytest.mark.parametrize("N,K", [(1536, 8960), (2048, 11008), (100, 8192), (8192, 8192),
-                                 (5120, 13824), (3584, 18944), (4100, 18944)])
+                                 (5120, 13824), (3584, 18944), (4100, 18944), (8000, 8192)])
 def test_gemv_m1_long_row_layouts(kernels, oracle, N, K):
     """M = 1 with long rows (K / 128 >= 64) in each layout the planner picks on MI355X's 256
-    CUs: one round of ceil(N / CUs) rows per CU when 16-row groups would fill half the CUs or
-    fewer (6, 8 and 1 rows), 16-row groups one per CU (224 and 257 groups: the last group short),
-    and 16-row groups persistent over two rounds (512, 320 groups)."""
+    CUs: one round of ceil(N / CUs) rows per CU on sixteen waves when 16-row groups would fill
+    half the CUs or fewer (6, 8 and 1 rows), 16-row groups one per CU (224 groups) and over two
+    full rounds (512 groups), and one round on fourteen waves between one and two rounds of
+    16-row groups (257, 320 and 500 groups: 17, 20 and 32 rows per CU)."""
     G = 128
     Wq, S = synth.weights(N, K, G, seed=N + 5 * K)
     X = synth.activations(1, K, seed=N + 13)
