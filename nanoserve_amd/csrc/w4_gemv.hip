@@ -38,6 +38,17 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t& v) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
+// Bytes of the scale array (N x C bf16) that a buffer resource covers in the kernels loading
+// scales 16 bytes at a time: rounded up to whole dwords. A dword load that reaches past the
+// resource's range reads as zero as a whole, so with N * C odd the array's last scale, which
+// shares a dword with the two bytes after the array, would read as zero. The launcher sends a
+// scale array that is not 4-byte aligned to another kernel in that case, so the two extra bytes
+// lie in the (4-byte aligned) dword that holds the last scale; they only ever land in the
+// scale slot of a row past N, whose output is not stored.
+__host__ __device__ inline int scale_span_bytes(int N, int C) {
+  return (int)((((size_t)N * C * 2) + 3) & ~(size_t)3);
+}
+
 // Row-tiled kernel: a wavefront owns RT 16-row tiles of W and a contiguous range of 128-k
 // chunks; the NW wavefronts of a workgroup split K and are reduced through LDS at the end.
 // Lane l = 16 h + r loads 16 bytes of row r (words 4h..4h+3 of the chunk) per chunk, so the
@@ -254,7 +265,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_xlds_kernel(
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(Wq), (short)0, (int)((size_t)N * (K >> 1)), 0x00020000);
   const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(S), (short)0, (int)((size_t)N * KG * 2), 0x00020000);
+      const_cast<uint16_t*>(S), (short)0, scale_span_bytes(N, KG), 0x00020000);
   const uint32_t rowb = (uint32_t)(K >> 1);
   auto issue = [&](u32x4_t (&w)[RT], int tile, int cw) {
     const bool live = tile < ntiles;
@@ -876,7 +887,7 @@ __global__ __launch_bounds__(NW * kWave) void w4_gemv_lds_kernel(
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint32_t*>(Wq), (short)0, (int)((size_t)N * RB), 0x00020000);
   const __amdgpu_buffer_rsrc_t sres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(S), (short)0, (int)((size_t)N * C * 2), 0x00020000);
+      const_cast<uint16_t*>(S), (short)0, scale_span_bytes(N, C), 0x00020000);
 
   // group g -> stage st: copy q (of 16 IPR + 1) is row q / IPR, bytes [1024 h, ...) with
   // h = q % IPR, or the group's 32 C scale bytes for q = 16 IPR. Wave w issues copies
@@ -1908,6 +1919,14 @@ hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t st, flo
       case 5: return launch_m8<5, 2, 2>(a, nw, 2, sp, st);
       default: return hipErrorInvalidValue;
     }
+  }
+  if ((p.lds || p.xlds) && ((size_t)a.N * (a.K >> 7)) % 2 != 0 &&
+      (reinterpret_cast<uintptr_t>(a.S) & 3) != 0) {
+    // the 16-byte scale loads of those kernels would need the two bytes after a scale array
+    // that is not 4-byte aligned (scale_span_bytes): the kernel with 2-byte scale loads
+    hipLaunchKernelGGL((w4_gemv_generic_kernel<8>), dim3((a.N + 3) / 4), dim3(256), 0, st, a.X,
+                       a.Wq, a.S, a.Y, a.M, a.N, a.K, a.G);
+    return hipSuccess;
   }
   if (p.lds) {
     // copies per wave per group: 16 rows x ceil(C / 16) row pieces + the scale slab

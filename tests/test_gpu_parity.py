@@ -399,6 +399,39 @@ def test_gemv_small_batch_odd_chunks(kernels, oracle, M, N, K):
     check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
 
 
+@pytest.mark.parametrize("M,N,K", [(8, 3521, 896), (3, 161, 1408), (5, 17, 384), (4, 333, 4224),
+                                   (7, 1001, 4480)])
+def test_gemv_small_batch_odd_scale_count(kernels, oracle, M, N, K):
+    """M = 2..8 where N x K / 128 is odd (odd N, odd chunk count): the kernels that load the scale
+    array 16 bytes at a time must still see its last scale, which shares a dword with the two
+    bytes after the array (up to 32 chunks: the LDS-staged kernel; beyond, the LDS-activation
+    kernel)."""
+    G = 128
+    Wq, S = synth.weights(N, K, G, seed=N + 3 * K + M)
+    X = synth.activations(M, K, seed=K + 5 * M, per_row_seed=True)
+    y = run_linear(kernels, X, Wq, S, G)
+    check_bf16_faithful(y, oracle.linear_f64(X, Wq, S, G), 2e-5)
+
+
+@pytest.mark.parametrize("M,N,K", [(8, 3521, 896), (4, 333, 4224)])
+def test_gemv_small_batch_unaligned_scales(kernels, oracle, M, N, K):
+    """The same shapes with the scale array at a 2-byte (not 4-byte) aligned address, as the C ABI
+    allows: the launcher takes the kernel with 2-byte scale loads there, so nothing past the
+    array is read, and the outputs stay faithful."""
+    G = 128
+    Wq, S = synth.weights(N, K, G, seed=N + 11 * K + M)
+    X = synth.activations(M, K, seed=K + 9 * M, per_row_seed=True)
+    C = K // G
+    sb = torch.zeros(N * C + 8, dtype=torch.bfloat16, device="cuda")
+    s_dev = sb[1:1 + N * C].view(N, C)
+    s_dev.copy_(to_dev(S, torch.bfloat16))
+    assert s_dev.data_ptr() % 4 == 2
+    y = kernels.w4_linear(to_dev(X, torch.bfloat16), to_dev(Wq, torch.int32), s_dev, G)
+    torch.cuda.synchronize()
+    yh = synth.bf16_bits_to_f32(to_host_bits(y)).astype(np.float64)
+    check_bf16_faithful(yh, oracle.linear_f64(X, Wq, S, G), 2e-5)
+
+
 @pytest.mark.parametrize("M,N,K", [(3, 4600, 3584), (7, 37880, 3584), (4, 3580, 3584), (6, 3577, 18944),
                                    (8, 9000, 7168)])
 def test_gemv_small_batch_group_heights(kernels, oracle, M, N, K):
