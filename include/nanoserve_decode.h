@@ -160,7 +160,7 @@ int ns_w4_gemv_decode(const void* X, const void* res, const void* r, const void*
  * pos, max_len, Hq and workspace: when that attention used more than one split of the cache
  * rows, their partial results are merged here (fp32, as the attention's own merge); otherwise
  * attn_out [K] bf16, which the attention then wrote, is read. Returns -2 for K != Hq * 128,
- * G != 128, max_len <= 0, NULL or misaligned pointers.
+ * G != 128, max_len <= 0, Hq > 64, NULL or misaligned pointers.
  */
 int ns_w4_gemv_decode_attn(const void* attn_out, const void* work, const int* pos, int max_len,
                            int Hq, const void* Wq, const void* S, void* Y, int N, int K, int G,

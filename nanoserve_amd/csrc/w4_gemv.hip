@@ -2002,15 +2002,22 @@ hipError_t launch_gemv_attn(const GemvArgs& a, const GemvPlan& p, const M1Fuse& 
   // the plain plan's seven-wave workgroups: fourteen here (one activation vector per thread)
   const int nw = L.nw == 7 ? 14 : L.nw;
   if (L.nw == 7) L.wpc = 2;
-  if (16 * CP > nw * kWave) {
-    *reject = 1;
-    return hipSuccess;
-  }
   M1Fuse fz = fz0;
   fz.rows = L.rows;
   // no activation-first barrier here: each workgroup reads every split's partials (115 KB at
   // 28 heads and 8 splits), and the weight stream should not queue behind them
   fz.xfirst = 0;
+  if (16 * CP > nw * kWave) {
+    // The merge needs one activation vector per thread. Where the plain layout's workgroups have
+    // fewer threads (50 to 63 heads: one round on fourteen waves, or eight-wave groups), the
+    // merging GEMV runs sixteen-wave workgroups of 16-row groups, two per CU, up to 64 heads; it
+    // reduces rows in the wide form, so it agrees with the plain GEMV to rounding, not in bits.
+    if (16 * CP > 16 * kWave) {
+      *reject = 1;
+      return hipSuccess;
+    }
+    return launch_m1<16, 2, 16, kXAttn, kYPlain, 1>(a, st, fz, 2);
+  }
   if (L.gr == 0) {
     // Where the plain layout is one round with up to 16 rows per CU (the o projection), the
     // attention-merging GEMV runs eight-wave workgroups of 16-row groups, two per CU: every

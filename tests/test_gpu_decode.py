@@ -307,6 +307,32 @@ def test_gemv_decode_attn_model_shapes(k, Hq, Hk, N):
     assert torch.equal(y, ref)
 
 
+@pytest.mark.parametrize("Hq,Hk,N", [(56, 8, 7168), (52, 13, 6656), (60, 10, 2048)])
+def test_gemv_decode_attn_wide_heads(k, Hq, Hk, N):
+    """50 to 63 query heads, where the plain GEMV's layout has fewer threads than the merged
+    activation has vectors: the merging GEMV takes sixteen-wave workgroups and agrees with the
+    merged attention output times the weights to one bf16 ulp, with one split and with several."""
+    D, max_len = 128, 700
+    qn, kn = Hq * D, Hk * D
+    Wq, S = _w4(N, qn, seed=Hq + 3 * N)
+    freq = R.inv_freq(D, 1000000.0).to(DEV)
+    work_a = k.decode_attention_workspace(Hq, Hk, D, max_len)
+    work_b = k.decode_attention_workspace(Hq, Hk, D, max_len)
+    kc, vc = rnd(Hk, max_len, D, seed=Hq + 4), rnd(Hk, max_len, D, seed=Hq + 5)
+    qkv = rnd(qn + 2 * kn, seed=Hq + 6, scale=0.5)
+    for pos in (50, 600):
+        print(f"gemv_decode_attn Hq={Hq} N={N} pos={pos}", flush=True)
+        p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+        merged = k.decode_qkv_attention(qkv, None, freq, p, kc, vc, Hq, Hk, D, work_a)
+        ref = k.w4_linear(merged, Wq, S, 128)
+        a = torch.empty_like(merged)
+        k.decode_qkv_attention(qkv, None, freq, p, kc, vc, Hq, Hk, D, work_b, out=a,
+                               merge=False)
+        y = k.gemv_decode_attn(a, work_b, p, max_len, Hq, Wq, S)
+        torch.cuda.synchronize()
+        close(y, ref.double().cpu(), rtol=2 ** -6, atol=2e-3 * ref.abs().max().item())
+
+
 # ------------------------------------------------------------------ ns_w4_gemv_decode
 def _w4(N, K, seed):
     """Quantized random weights (GPU), as the runner's: N(0, 0.02) bf16 through the quantizer."""
