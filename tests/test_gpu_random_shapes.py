@@ -75,3 +75,62 @@ def test_gemv_decode_random_shapes(kernels, oracle, M, N, K, G):
     torch.cuda.synchronize()
     assert torch.equal(y.reshape(-1), yd.reshape(-1))
     _faithful(_host(yd).reshape(1, -1), oracle.linear_f64(X, Wq, S, G))
+
+
+def _decode_cases(n=16, seed=7):
+    rng = random.Random(seed)
+    out = []
+    while len(out) < n:
+        K = 128 * rng.choice([1, 2, 3, 7, 8, 12, 14, 20, 28, 40, 56, 64, 100, 128])
+        N = 16 * rng.randint(1, rng.choice([8, 200, 2500]))
+        if N * K > 60_000_000:
+            continue
+        out.append((N, K, rng.choice(["norm_add", "swiglu_norm"])))
+    return out
+
+
+@pytest.mark.parametrize("N,K,mode", _decode_cases())
+def test_gemv_decode_fused_random_shapes(kernels, N, K, mode):
+    """The fused decode GEMV (add + RMSNorm in; SwiGLU out for gate/up rows interleaved in
+    blocks of 8) on random shapes: the new residual stream bit-exact against the oracle, the
+    output against the oracle-normalised activation's float64 product
+    and, for K <= 8192, against the unfused kernels (ns_rmsnorm, ns_w4_linear, ns_swiglu) to one
+    bf16 ulp."""
+    from oracle import decode_ref as R
+    from oracle import w4_oracle as O
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(N + K)
+    Wd = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    Wq, S = kernels.w4_quantize(Wd, 128)
+    del Wd
+    res = (torch.randn(K, generator=g) * 3.0).to(torch.bfloat16).to(dev)
+    r = torch.randn(K, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(K, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    res_out = torch.empty(K, dtype=torch.bfloat16, device=dev)
+    sw = mode == "swiglu_norm"
+    y = kernels.gemv_decode(Wq, S, 128, res=res, r=r, norm_w=w, eps=1e-6, res_out=res_out,
+                            swiglu=sw)
+    torch.cuda.synchronize()
+    v_ref, h_ref = R.rmsnorm(res.reshape(1, -1), r.reshape(1, -1), w, 1e-6)
+    assert torch.equal(res_out.double().cpu(), v_ref.reshape(-1))
+    hb = R.bf16_round(h_ref).to(torch.bfloat16).reshape(1, -1)
+    ref = torch.from_numpy(O.linear_f64(hb.view(torch.int16).numpy().view("uint16"),
+                                        Wq.cpu().numpy().view("uint32"),
+                                        S.cpu().view(torch.int16).numpy().view("uint16"), 128))
+    if sw:
+        g4 = ref.view(N // 16, 2, 8)
+        gate, up = R.bf16_round(g4[:, 0].reshape(-1)), R.bf16_round(g4[:, 1].reshape(-1))
+        ref = (gate / (1.0 + torch.exp(-gate)) * up).reshape(1, -1)
+    err = (y.double().cpu() - ref).abs().max().item()
+    assert err <= 1e-2 * ref.abs().max().item(), err
+    if K <= 8192:  # ns_rmsnorm's own limit (the reference's: H <= 8192)
+        h = kernels.rmsnorm(res.clone().reshape(1, -1), r.reshape(1, -1), w, 1e-6)
+        gu = kernels.w4_linear(h, Wq, S, 128)
+        if sw:
+            u4 = gu.view(N // 16, 2, 8)
+            gu = kernels.swiglu(u4[:, 0].reshape(1, -1).contiguous(),
+                                u4[:, 1].reshape(1, -1).contiguous())
+        torch.cuda.synchronize()
+        torch.testing.assert_close(y.double().cpu(), gu.double().cpu(), rtol=2 ** -7,
+                                   atol=1e-3 * gu.abs().max().item())
