@@ -1738,7 +1738,9 @@ struct M1Layout {
 //   32 blocks or where 14 fits C up to 28 blocks, else sixteen (qkv 5.71 -> 4.68, o 4.68 -> 4.41
 //   against 16-row groups at eight waves, two per CU; 5120 x 5120 6.92 -> 5.54 and 6144 x 4096
 //   5.92 -> 5.47 likewise; with 1120 groups, 17920 x 1536, 16-row groups stay ahead: 5.99
-//   against 6.52 in one round).
+//   against 6.52 in one round). One round as two workgroups per CU of half the rows each (eight
+//   or seven waves, with or without the activation first) is slower: qkv 4.69 against
+//   4.98-5.75, o 4.43 against 4.69-4.85; so are three-slot rings (qkv 5.32-5.39, o 4.88-5.30).
 // * Otherwise eight waves per 16-row group (8-row groups when 16-row ones would give each CU
 //   only one or two), two workgroups per CU.
 hipError_t m1_layout(int N, int K, M1Layout* L) {
